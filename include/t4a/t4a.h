@@ -1,0 +1,193 @@
+/*
+ * t4a MI355X host C ABI: checked launch planning and the HIP launchers of the
+ * movement and single-axis reduction entries.
+ *
+ * The reference splits its boundary in two: a Rust host planner
+ * (reference src/lib.rs) that validates metadata and returns launch geometry,
+ * and `extern "C" __global__` kernels (reference cuda/src/movement.cu,
+ * cuda/src/reduce.cu) that the caller launches on its own stream with that
+ * geometry. This library keeps both halves behind plain C functions:
+ *
+ *   t4a_plan_*     restate the reference planners (same validation order, same
+ *                  error for the same bad input) and return MI355X geometry;
+ *   t4a_hip_*      launch the gfx950 kernel of the same name on the caller's
+ *                  stream with a planned geometry (the reference caller's
+ *                  cuLaunchKernel, tests/gpu/mod.rs:297-324).
+ *
+ * Ownership is the reference's (docs/abi/c-kernel-abi.md:3-14): the caller owns
+ * the device, stream, every buffer and the partials workspace, and decides when
+ * to synchronize. Nothing here allocates device memory or synchronizes.
+ *
+ * Status values: 0 is success; otherwise the reference `Error` discriminant
+ * plus one (reference src/lib.rs:217-274), or one of the T4A_HIP_* launch
+ * statuses below. Rank is bounded by T4A_CUDA_MAX_RANK (the reference's fast
+ * path, `Layout`/`CLayout`).
+ */
+#ifndef T4A_T4A_H_
+#define T4A_T4A_H_
+
+#include "t4a/abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  T4A_OK = 0,
+  T4A_ERR_RANK_OUT_OF_RANGE = 1,
+  T4A_ERR_RANK_LENGTH = 2,
+  T4A_ERR_NEGATIVE_EXTENT = 3,
+  T4A_ERR_NEGATIVE_COUNT = 4,
+  T4A_ERR_OVERFLOW = 5,
+  T4A_ERR_COUNT_MISMATCH = 6,
+  T4A_ERR_OFFSET_OUT_OF_SPAN = 7,
+  T4A_ERR_BROADCAST_DESTINATION = 8,
+  T4A_ERR_UNSUPPORTED_DTYPE = 9,
+  T4A_ERR_NOT_ELEMENTWISE = 10,
+  T4A_ERR_LAUNCH_LIMIT = 11,
+  T4A_ERR_INVALID_TRANSPOSE_CONFIG = 12,
+  T4A_ERR_INVALID_AXIS = 13,
+  T4A_ERR_DUPLICATE_AXIS = 14,
+  T4A_ERR_NOT_COMPACT = 15,
+  T4A_ERR_SHAPE_MISMATCH = 16,
+  T4A_ERR_INVALID_STEP = 17,
+  T4A_ERR_INVALID_PADDING = 18,
+  T4A_ERR_DOMAIN_TOO_LARGE = 19,
+  T4A_ERR_INVALID_STRIDE = 20,
+  T4A_ERR_STRATEGY_MISMATCH = 21,
+  T4A_ERR_INVALID_PLANE_WIDTH = 22,
+  T4A_ERR_INVALID_SPLIT = 23,
+  T4A_ERR_INDEX_VECTOR_MISMATCH = 24,
+  T4A_ERR_UNSUPPORTED_OP = 25,
+  /* Launch-side statuses of the t4a_hip_* functions (no reference counterpart:
+   * the reference returns nothing from a raw launch). */
+  T4A_HIP_ERR_LAUNCH = 100,       /* the HIP runtime refused the launch */
+  T4A_HIP_ERR_NULL_ARGUMENT = 101 /* a required pointer argument is NULL */
+} t4a_status;
+
+/* Reference RankVariant (src/lib.rs:800-838): FAST selects the by-value symbol. */
+typedef enum { T4A_VARIANT_FAST = 0, T4A_VARIANT_GENERAL = 1 } t4a_rank_variant;
+
+/* Reference Launch (src/lib.rs:840-873). Any zero grid dimension means "no
+ * work": the caller (and every t4a_hip_* launcher) skips the launch. */
+typedef struct {
+  unsigned int grid[3];
+  unsigned int block[3];
+  unsigned int shared_bytes;
+  int variant;
+} t4a_launch;
+
+/* Reference Split (src/lib.rs:3146-3150). */
+typedef struct {
+  long long splits;
+  long long chunk_len;
+} t4a_split;
+
+typedef enum { T4A_PLAN_DIRECT = 0, T4A_PLAN_SPLIT = 1 } t4a_reduction_plan_kind;
+
+/* Reference ReductionPlan (src/lib.rs:3168-3182). DIRECT fills `strategy` and
+ * `launch`; SPLIT fills `split`, `pass1`, `combine_strategy`, `combine_op` and
+ * `pass2`. */
+typedef struct {
+  int kind;
+  int strategy;
+  t4a_launch launch;
+  t4a_split split;
+  t4a_launch pass1;
+  int combine_strategy;
+  int combine_op;
+  t4a_launch pass2;
+} t4a_reduction_plan;
+
+/* ---- library facts ---------------------------------------------------------- */
+
+int t4a_abi_revision(void);                 /* T4A_CUDA_ABI_REVISION */
+const char* t4a_status_name(int status);    /* "OffsetOutOfSpan", ..., "Ok" */
+int t4a_dtype_size(int dtype);              /* reference DType::size; 0 if unknown */
+
+/* ---- layouts (reference Layout, src/lib.rs:322-450) -------------------------- */
+
+/* Build a layout of `rank` axes; the unused slots are zeroed.
+ * Errors: RankOutOfRange (rank > 8 or < 0), NegativeExtent. */
+int t4a_layout_new(t4a_cuda_layout* out, int rank, const long long* extents,
+                   const long long* strides, long long offset);
+/* Compact layout over `extents`, axis 0 fastest. Errors: as above, Overflow. */
+int t4a_layout_compact(t4a_cuda_layout* out, int rank, const long long* extents);
+/* Checked extent product (reference Layout::element_count). */
+int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count);
+
+/* ---- movement planners (reference src/lib.rs:1628-1737) ---------------------- */
+
+int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
+                                 t4a_launch* launch);
+int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
+                                const t4a_cuda_layout* dst, long long dst_len,
+                                t4a_launch* launch);
+/* Reference TransposeConfig::new (src/lib.rs:471-491). */
+int t4a_transpose_config_new(int tile, int block_rows, int padding, int vector_width,
+                             t4a_cuda_transpose_config* config);
+/* The reference default configuration {16, 8, 1, 1} (src/lib.rs:463-468). */
+t4a_cuda_transpose_config t4a_transpose_config_default(void);
+int t4a_plan_tiled_transpose(int dtype, t4a_cuda_transpose_config config, long long src_offset,
+                             long long batch_stride, long long dst_fast_extent,
+                             long long src_fast_extent, long long batches, long long src_len,
+                             long long dst_len, t4a_launch* launch);
+
+/* ---- reduction planners (reference src/lib.rs:3031-3557) ---------------------- */
+
+/* `*has_split` is 0 when the axis takes one pass (reference Ok(None)). */
+int t4a_split_policy(long long reduce_len, unsigned int plane_width, int* has_split,
+                     t4a_split* split);
+int t4a_plan_reduce(int dtype, int op, int strategy, const t4a_cuda_layout* out_layout,
+                    long long out_len, const t4a_cuda_layout* in_layout, long long in_len,
+                    unsigned int axis, unsigned int plane_width, t4a_launch* launch);
+int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_layout,
+                             long long partials_len, const t4a_cuda_layout* in_layout,
+                             long long in_len, unsigned int axis, t4a_split split,
+                             unsigned int plane_width, t4a_launch* launch);
+int t4a_plan_reduction(int dtype, int op, const t4a_cuda_layout* out_layout, long long out_len,
+                       const t4a_cuda_layout* in_layout, long long in_len, unsigned int axis,
+                       unsigned int plane_width, t4a_reduction_plan* plan);
+/* Compact partials layout: the input's extents with the axis set to `splits`
+ * (reference reduction_partials_layout, src/lib.rs:3530-3557). */
+int t4a_reduction_partials_layout(const t4a_cuda_layout* in_layout, unsigned int axis,
+                                  long long splits, t4a_cuda_layout* partials_layout);
+
+/* ---- HIP launchers ------------------------------------------------------------
+ * Each launches the gfx950 kernel of the reference entry's name with the
+ * arguments of that entry, on `stream` (a hipStream_t; NULL is the null stream),
+ * using `launch` as returned by the matching planner. An empty launch returns
+ * T4A_OK without touching the device. Metadata is not re-validated here (the
+ * reference raw entry is caller UB past its planner, c-kernel-abi.md:9-14).
+ */
+
+/* Reference t4a_cuda_tiled_transpose, cuda/src/movement.cu:571-573. */
+int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype, long long src_offset,
+                            long long batch_stride, long long dst_fast_extent,
+                            long long src_fast_extent, t4a_cuda_transpose_config config,
+                            const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_materialize_strided, cuda/src/movement.cu:535-537. */
+int t4a_hip_materialize_strided(void* dst, const void* src, int dtype,
+                                const t4a_cuda_layout* src_layout, long long len,
+                                const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_strided_to_strided, cuda/src/movement.cu:553-556. */
+int t4a_hip_strided_to_strided(void* dst, const void* src, int dtype,
+                               const t4a_cuda_layout* src_layout,
+                               const t4a_cuda_layout* dst_layout, long long len,
+                               const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_reduce, cuda/src/reduce.cu:765-768. */
+int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int strategy,
+                   const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
+                   int axis, long long output_len, const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_reduce_partials, cuda/src/reduce.cu:813-817. */
+int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
+                            const t4a_cuda_layout* partials_layout,
+                            const t4a_cuda_layout* in_layout, int axis, long long output_len,
+                            long long splits, long long chunk_len, const t4a_launch* launch,
+                            void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* T4A_T4A_H_ */

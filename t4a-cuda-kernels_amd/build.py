@@ -1,0 +1,87 @@
+"""Build libt4a_hip.so: the gfx950 kernels, their launchers and the host planner.
+
+Run `python t4a-cuda-kernels_amd/build.py` (or `__graft_entry__.build()`). The
+shared library is written next to the Python package
+(`t4a_cuda_kernels/libt4a_hip.so`) so that it travels with the source tree.
+
+HIP sources are compiled for gfx950 only, with:
+  -ffp-contract=off      every floating-point rounding is the one written
+                         (the fold topology and the complex product spell
+                         out their fused multiply-adds);
+  -packed-fp32-ops off   no packed FP32 instructions are generated.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent
+REPO = PKG_ROOT.parent
+CSRC = PKG_ROOT / "csrc"
+OUT_DIR = PKG_ROOT / "t4a_cuda_kernels"
+LIB_NAME = "libt4a_hip.so"
+ARCH = "gfx950"
+
+HIP_SOURCES = ["movement.hip", "reduce.hip"]
+CXX_SOURCES = ["planner.cpp"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link the shared library; returns its path."""
+    hipcc = _hipcc()
+    obj_dir = PKG_ROOT / "_build"
+    obj_dir.mkdir(exist_ok=True)
+    includes = [f"-I{REPO / 'include'}", f"-I{CSRC}"]
+    objects = []
+    for src in CXX_SOURCES:
+        obj = obj_dir / (Path(src).stem + ".o")
+        cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", *includes,
+               "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd))
+        _run(cmd)
+        objects.append(obj)
+    hip_flags = [
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+        "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+    ]
+    for src in HIP_SOURCES:
+        obj = obj_dir / (Path(src).stem + ".o")
+        cmd = [hipcc, *hip_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd))
+        _run(cmd)
+        objects.append(obj)
+    OUT_DIR.mkdir(exist_ok=True)
+    out = OUT_DIR / LIB_NAME
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects),
+           "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,207 @@
+// Device element arithmetic, fold objects and 32-lane plane collectives for
+// gfx950.
+//
+// The arithmetic restates the reference's element semantics
+// (reference cuda/include/t4a/abi.cuh:590-818): wrapping integer sum and
+// product, IEEE float and componentwise complex arithmetic, a square rounded
+// before it is added, and NaN-propagating extrema that order -0 below +0. All
+// HIP sources are built with -ffp-contract=off, so every rounding is the one
+// written here; the complex product spells out its fused multiply-adds.
+#ifndef T4A_DEVICE_H_
+#define T4A_DEVICE_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "geometry.h"
+
+namespace t4a {
+
+using c32 = t4a_cuda_c32;
+using c64 = t4a_cuda_c64;
+
+// ---- element arithmetic ------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ T add(T a, T b) { return a + b; }
+template <>
+__device__ __forceinline__ int add<int>(int a, int b) {
+  return static_cast<int>(static_cast<unsigned>(a) + static_cast<unsigned>(b));
+}
+template <>
+__device__ __forceinline__ long long add<long long>(long long a, long long b) {
+  return static_cast<long long>(static_cast<unsigned long long>(a) +
+                                static_cast<unsigned long long>(b));
+}
+template <>
+__device__ __forceinline__ c32 add<c32>(c32 a, c32 b) { return c32{a.re + b.re, a.im + b.im}; }
+template <>
+__device__ __forceinline__ c64 add<c64>(c64 a, c64 b) { return c64{a.re + b.re, a.im + b.im}; }
+
+template <typename T>
+__device__ __forceinline__ T mul(T a, T b) { return a * b; }
+template <>
+__device__ __forceinline__ int mul<int>(int a, int b) {
+  return static_cast<int>(static_cast<unsigned>(a) * static_cast<unsigned>(b));
+}
+template <>
+__device__ __forceinline__ long long mul<long long>(long long a, long long b) {
+  return static_cast<long long>(static_cast<unsigned long long>(a) *
+                                static_cast<unsigned long long>(b));
+}
+// (a.re*b.re - a.im*b.im, a.re*b.im + a.im*b.re) with one product of each
+// component fused: re = fma(a.re, b.re, -(a.im*b.im)), im = fma(a.im, b.re,
+// a.re*b.im). This is the rounding of the reference build's contracted complex
+// product, written out explicitly (the reference's A100 golden vectors select
+// it among the possible contractions).
+template <>
+__device__ __forceinline__ c32 mul<c32>(c32 a, c32 b) {
+  const float ii = a.im * b.im;
+  const float ri = a.re * b.im;
+  return c32{__builtin_fmaf(a.re, b.re, -ii), __builtin_fmaf(a.im, b.re, ri)};
+}
+template <>
+__device__ __forceinline__ c64 mul<c64>(c64 a, c64 b) {
+  const double ii = a.im * b.im;
+  const double ri = a.re * b.im;
+  return c64{__builtin_fma(a.re, b.re, -ii), __builtin_fma(a.im, b.re, ri)};
+}
+
+// A square rounded once, before any later addition.
+template <typename T>
+__device__ __forceinline__ T square(T v) { return v; }
+template <>
+__device__ __forceinline__ float square<float>(float v) { return __builtin_fmaf(v, v, 0.0f); }
+template <>
+__device__ __forceinline__ double square<double>(double v) { return __builtin_fma(v, v, 0.0); }
+
+// NaN wins (lhs first); equal operands differ at most in the sign of zero, and
+// the maximum keeps +0 (AND of the bit patterns), the minimum -0 (OR).
+__device__ __forceinline__ float fmax_nan(float l, float r) {
+  const float both = __uint_as_float(__float_as_uint(l) & __float_as_uint(r));
+  const float ordered = l == r ? both : (r > l ? r : l);
+  const float right = r != r ? r : ordered;
+  return l != l ? l : right;
+}
+__device__ __forceinline__ float fmin_nan(float l, float r) {
+  const float either = __uint_as_float(__float_as_uint(l) | __float_as_uint(r));
+  const float ordered = l == r ? either : (r < l ? r : l);
+  const float right = r != r ? r : ordered;
+  return l != l ? l : right;
+}
+__device__ __forceinline__ double fmax_nan(double l, double r) {
+  const double both =
+      __longlong_as_double(__double_as_longlong(l) & __double_as_longlong(r));
+  const double ordered = l == r ? both : (r > l ? r : l);
+  const double right = r != r ? r : ordered;
+  return l != l ? l : right;
+}
+__device__ __forceinline__ double fmin_nan(double l, double r) {
+  const double either =
+      __longlong_as_double(__double_as_longlong(l) | __double_as_longlong(r));
+  const double ordered = l == r ? either : (r < l ? r : l);
+  const double right = r != r ? r : ordered;
+  return l != l ? l : right;
+}
+
+template <typename T>
+__device__ __forceinline__ T vmax(T a, T b) { return a > b ? a : b; }
+template <typename T>
+__device__ __forceinline__ T vmin(T a, T b) { return a < b ? a : b; }
+template <>
+__device__ __forceinline__ float vmax<float>(float a, float b) { return fmax_nan(a, b); }
+template <>
+__device__ __forceinline__ float vmin<float>(float a, float b) { return fmin_nan(a, b); }
+template <>
+__device__ __forceinline__ double vmax<double>(double a, double b) { return fmax_nan(a, b); }
+template <>
+__device__ __forceinline__ double vmin<double>(double a, double b) { return fmin_nan(a, b); }
+
+// ---- folds ---------------------------------------------------------------------
+// seed(v): the accumulator's first value; fold(acc, v): one more element;
+// combine(a, b): two accumulators. Only SUM_SQUARES tells fold and combine apart
+// (reference cuda/src/reduce.cu:25-108). kRegroup: pass 1 may take the grouped
+// walk (every fold except PROD).
+
+struct SumFold {
+  static constexpr bool kRegroup = true;
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const { return add(a, v); }
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const { return add(a, b); }
+};
+struct ProdFold {
+  static constexpr bool kRegroup = false;
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const { return mul(a, v); }
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const { return mul(a, b); }
+};
+struct SumSquaresFold {
+  static constexpr bool kRegroup = true;
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return square(v); }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const { return add(a, square(v)); }
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const { return add(a, b); }
+};
+struct MaxFold {
+  static constexpr bool kRegroup = true;
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const { return vmax(a, v); }
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const { return vmax(a, b); }
+};
+struct MinFold {
+  static constexpr bool kRegroup = true;
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const { return vmin(a, v); }
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const { return vmin(a, b); }
+};
+
+// ---- lane exchange ---------------------------------------------------------------
+// xor exchange inside aligned groups of `width` lanes of the 64-lane wavefront.
+
+__device__ __forceinline__ float shfl_xor(float v, int m, int w) { return __shfl_xor(v, m, w); }
+__device__ __forceinline__ double shfl_xor(double v, int m, int w) { return __shfl_xor(v, m, w); }
+__device__ __forceinline__ int shfl_xor(int v, int m, int w) { return __shfl_xor(v, m, w); }
+__device__ __forceinline__ long long shfl_xor(long long v, int m, int w) {
+  return __shfl_xor(v, m, w);
+}
+__device__ __forceinline__ c32 shfl_xor(c32 v, int m, int w) {
+  return c32{__shfl_xor(v.re, m, w), __shfl_xor(v.im, m, w)};
+}
+__device__ __forceinline__ c64 shfl_xor(c64 v, int m, int w) {
+  return c64{__shfl_xor(v.re, m, w), __shfl_xor(v.im, m, w)};
+}
+
+// The plane xor tree: offsets 1, 2, 4, ... < width, each lane combining its own
+// value (left) with its partner's (reference reduce.cu:148-157). Lane 0 ends
+// with the own-left pairwise tree of the plane's lanes.
+template <typename Fold, typename T>
+__device__ __forceinline__ T plane_tree(T v, int width, Fold f) {
+  for (int off = 1; off < width; off <<= 1) v = f.combine(v, shfl_xor(v, off, width));
+  return v;
+}
+
+// Pairwise own-left tree over `n` register values (n a power of two); the
+// value of lane 0 of a plane whose lanes are held by one thread.
+template <int N, typename Fold, typename T>
+__device__ __forceinline__ T register_tree(T* v, Fold f) {
+#pragma unroll
+  for (int off = 1; off < N; off <<= 1) {
+#pragma unroll
+    for (int l = 0; l < N; l += 2 * off) v[l] = f.combine(v[l], v[l + off]);
+  }
+  return v[0];
+}
+
+// ---- vector payloads -----------------------------------------------------------
+
+struct alignas(16) Bits128 {
+  unsigned long long lo, hi;
+};
+// A 16-byte element that is only 8-byte aligned (c64).
+struct alignas(8) Elem16 {
+  unsigned long long lo, hi;
+};
+
+}  // namespace t4a
+
+#endif  // T4A_DEVICE_H_

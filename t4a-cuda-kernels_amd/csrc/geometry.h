@@ -1,0 +1,373 @@
+// Launch-independent work decompositions shared by the host planner and the
+// gfx950 kernels. Every function here is a pure function of an entry's
+// arguments, so the planner (which sizes the grid) and the kernel (which walks
+// the work) always agree. The kernels walk their work items with grid-stride
+// loops, so any geometry computes the same result; the planned one is the fast
+// one.
+//
+// Nothing here changes *what* an entry computes: movement is a bijection of
+// logical coordinates, and the reductions keep the reference's per-element fold
+// order (which lane of which plane folds which element, reference
+// cuda/src/reduce.cu:343-633). Only the mapping of that work onto MI355X
+// wavefronts is chosen here.
+#ifndef T4A_GEOMETRY_H_
+#define T4A_GEOMETRY_H_
+
+#include "t4a/abi.h"
+
+#if defined(__HIP__)
+#define T4A_HD __host__ __device__ __forceinline__
+#else
+#define T4A_HD inline
+#endif
+
+namespace t4a {
+
+// Threads per block of every MI355X launch this library plans (four 64-lane
+// wavefronts).
+constexpr int kBlock = 256;
+constexpr int kWave = 64;
+// Lanes of a reference "warp": planes wider than this cross it (reduce.cu:140).
+constexpr int kWarp = 32;
+
+T4A_HD int dtype_size(int dtype) {
+  switch (dtype) {
+    case T4A_CUDA_F32: return 4;
+    case T4A_CUDA_F64: return 8;
+    case T4A_CUDA_I32: return 4;
+    case T4A_CUDA_I64: return 8;
+    case T4A_CUDA_BOOL: return 1;
+    case T4A_CUDA_C32: return 8;
+    case T4A_CUDA_C64: return 16;
+    default: return 0;
+  }
+}
+
+// ---- tiled transpose ----------------------------------------------------------
+//
+// dst[b*S + i + j*M] = src[src_offset + b*S + i*N + j] (reference
+// docs/abi/c-kernel-abi.md:151-159). A tile is kTileM source rows (i) by
+// kTileN source columns (j), staged through LDS; tile index order is i-tile
+// fastest, then j-tile, then batch, like the reference's (x, y, z) grid.
+struct TransposeTiling {
+  int tile_m;
+  int tile_n;
+  long long tiles_m;
+  long long tiles_n;
+  long long total;  // tiles over all batches
+};
+
+T4A_HD TransposeTiling transpose_tiling(long long m, long long n, long long batches,
+                                        int esize) {
+  TransposeTiling t;
+  // 64x64 elements for 1-8 byte elements (16-32 KiB of LDS), 32x64 for 16-byte
+  // ones, so one tile row is a 256-1024 byte HBM segment on both sides.
+  t.tile_m = 64;
+  t.tile_n = esize >= 16 ? 32 : 64;
+  t.tiles_m = (m + t.tile_m - 1) / t.tile_m;
+  t.tiles_n = (n + t.tile_n - 1) / t.tile_n;
+  t.total = t.tiles_m * t.tiles_n * batches;
+  return t;
+}
+
+// ---- strided movement -----------------------------------------------------------
+//
+// Both movement entries copy every logical coordinate of a shared extent set
+// from a source layout to a destination layout. The plan fuses the axes into at
+// most eight "dims" (extent-one axes dropped, axes contiguous in both layouts
+// merged), then picks:
+//   TILED   the destination-contiguous run (dims chained from the dim of
+//           destination stride 1) differs from the source-contiguous run
+//           (chained from the dim of source stride 1): an LA x LB tile through
+//           LDS, read along the source run and written along the destination run;
+//   CONTIG  the same dim is contiguous on both sides: row copies;
+//   GENERIC anything else (broadcast or reversed fast axes): per-element decode.
+enum MoveMode { kMoveEmpty = 0, kMoveGeneric = 1, kMoveContig = 2, kMoveTiled = 3 };
+
+constexpr int kMaxDims = T4A_CUDA_MAX_RANK;
+
+struct MovePlan {
+  int mode;
+  int n;                      // fused dims
+  long long ext[kMaxDims];
+  long long ss[kMaxDims];     // source strides
+  long long ds[kMaxDims];     // destination strides
+  long long src_offset;
+  long long dst_offset;
+  long long len;              // logical elements
+  // TILED: the A chain (destination run) is dims a_dims[0..na), the last one
+  // tiled by a_tile; the B chain (source run) is b_dims[0..nb), the last tiled
+  // by b_tile. la/lb are the run lengths of a full tile.
+  int na, nb;
+  int a_dims[kMaxDims];
+  int b_dims[kMaxDims];
+  long long a_tile, b_tile;
+  long long la, lb;
+  long long a_inner, b_inner;  // product of full extents before the tiled dim
+  // Batch dims: every dim outside both chains, plus the two tiled dims' tile
+  // counts, walked with the A tile count fastest.
+  int nbatch;
+  int batch_dims[kMaxDims];
+  long long a_tiles, b_tiles;
+  long long tiles;            // total work items (tiles, rows or elements)
+  // CONTIG: dim `row_dim` is contiguous on both sides; rows are decoded over
+  // the other dims.
+  int row_dim;
+  long long row_len;
+  long long rows;
+};
+
+T4A_HD int move_chain_contains(const int* dims, int count, int dim) {
+  for (int i = 0; i < count; ++i) {
+    if (dims[i] == dim) return 1;
+  }
+  return 0;
+}
+
+// `dst_strides == nullptr` means the compact destination of materialize_strided.
+T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* dst_strides,
+                      long long dst_offset, long long len, int esize) {
+  p->mode = kMoveEmpty;
+  p->n = 0;
+  p->len = len;
+  p->src_offset = src.offset;
+  p->dst_offset = dst_offset;
+  p->na = p->nb = p->nbatch = 0;
+  p->tiles = 0;
+  p->row_dim = -1;
+  if (len <= 0) return;
+  int rank = src.rank;
+  if (rank < 0) rank = 0;
+  if (rank > kMaxDims) rank = kMaxDims;
+  long long compact = 1;
+  for (int k = 0; k < rank; ++k) {
+    const long long e = src.extents[k];
+    const long long s = src.strides[k];
+    const long long d = dst_strides ? dst_strides[k] : compact;
+    compact *= e;
+    if (e == 1) continue;
+    if (p->n > 0) {
+      const int last = p->n - 1;
+      if (s == p->ss[last] * p->ext[last] && d == p->ds[last] * p->ext[last]) {
+        p->ext[last] *= e;
+        continue;
+      }
+    }
+    p->ext[p->n] = e;
+    p->ss[p->n] = s;
+    p->ds[p->n] = d;
+    ++p->n;
+  }
+  if (p->n == 0) {  // one element (rank 0 or all extents one)
+    p->mode = kMoveGeneric;
+    p->tiles = 1;
+    return;
+  }
+  int a = -1, b = -1;
+  for (int k = 0; k < p->n; ++k) {
+    if (p->ds[k] == 1 && a < 0) a = k;
+    if (p->ss[k] == 1 && b < 0) b = k;
+  }
+  if (a >= 0 && a == b) {
+    p->mode = kMoveContig;
+    p->row_dim = a;
+    p->row_len = p->ext[a];
+    p->rows = len / p->row_len;
+    p->tiles = p->rows;
+    return;
+  }
+  if (a < 0 || b < 0) {
+    p->mode = kMoveGeneric;
+    p->tiles = len;
+    return;
+  }
+  // Tile budget: 4096 elements up to 8 bytes (<= 32 KiB of LDS), 2048 for
+  // 16-byte elements; each run aims for 64 elements.
+  const long long target_a = 64;
+  const long long target_b = esize >= 16 ? 32 : 64;
+  // Grow a run along its chain: each next dim's stride on that side equals the
+  // run's span so far; a dim of the other chain ends it.
+  p->a_dims[0] = a;
+  p->na = 1;
+  p->b_dims[0] = b;
+  p->nb = 1;
+  {
+    long long span = p->ext[a];
+    while (span < target_a) {
+      int next = -1;
+      for (int k = 0; k < p->n; ++k) {
+        if (p->ds[k] == span && !move_chain_contains(p->a_dims, p->na, k) && k != b) next = k;
+      }
+      if (next < 0) break;
+      p->a_dims[p->na++] = next;
+      span *= p->ext[next];
+    }
+  }
+  {
+    long long span = p->ext[b];
+    while (span < target_b) {
+      int next = -1;
+      for (int k = 0; k < p->n; ++k) {
+        if (p->ss[k] == span && !move_chain_contains(p->b_dims, p->nb, k) &&
+            !move_chain_contains(p->a_dims, p->na, k))
+          next = k;
+      }
+      if (next < 0) break;
+      p->b_dims[p->nb++] = next;
+      span *= p->ext[next];
+    }
+  }
+  // Tile the last dim of each chain so that the run stays near its target.
+  p->a_inner = 1;
+  for (int i = 0; i + 1 < p->na; ++i) p->a_inner *= p->ext[p->a_dims[i]];
+  {
+    const long long last = p->ext[p->a_dims[p->na - 1]];
+    long long t = target_a / p->a_inner;
+    if (t < 1) t = 1;
+    if (t > last) t = last;
+    p->a_tile = t;
+    p->a_tiles = (last + t - 1) / t;
+    p->la = p->a_inner * t;
+  }
+  p->b_inner = 1;
+  for (int i = 0; i + 1 < p->nb; ++i) p->b_inner *= p->ext[p->b_dims[i]];
+  {
+    const long long last = p->ext[p->b_dims[p->nb - 1]];
+    long long t = target_b / p->b_inner;
+    if (t < 1) t = 1;
+    if (t > last) t = last;
+    p->b_tile = t;
+    p->b_tiles = (last + t - 1) / t;
+    p->lb = p->b_inner * t;
+  }
+  long long tiles = p->a_tiles * p->b_tiles;
+  for (int k = 0; k < p->n; ++k) {
+    if (move_chain_contains(p->a_dims, p->na, k) || move_chain_contains(p->b_dims, p->nb, k))
+      continue;
+    p->batch_dims[p->nbatch++] = k;
+    tiles *= p->ext[k];
+  }
+  p->mode = kMoveTiled;
+  p->tiles = tiles;
+}
+
+// ---- reductions ---------------------------------------------------------------
+//
+// The non-axis axes of a reduction, fused: extent-one axes dropped and
+// neighbours merged where both the input and the output (or partials) strides
+// continue each other. The output index decodes over them in axis order, as
+// reduce.cu:110-130 decodes it over the output layout.
+struct ReduceDims {
+  int n;
+  long long ext[kMaxDims];
+  long long is[kMaxDims];  // input strides
+  long long os[kMaxDims];  // output / partials strides
+  long long in_offset;
+  long long out_offset;
+  long long axis_len;
+  long long axis_stride;
+  long long out_axis_stride;  // partials stride of the split coordinate
+};
+
+T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
+                        const t4a_cuda_layout& in, int axis) {
+  r->n = 0;
+  r->in_offset = in.offset;
+  r->out_offset = out.offset;
+  r->axis_len = in.extents[axis];
+  r->axis_stride = in.strides[axis];
+  r->out_axis_stride = out.strides[axis];
+  int rank = out.rank;
+  if (rank > kMaxDims) rank = kMaxDims;
+  for (int k = 0; k < rank; ++k) {
+    if (k == axis) continue;
+    const long long e = out.extents[k];
+    if (e == 1) continue;
+    const long long s = in.strides[k];
+    const long long o = out.strides[k];
+    if (r->n > 0) {
+      const int last = r->n - 1;
+      if (s == r->is[last] * r->ext[last] && o == r->os[last] * r->ext[last]) {
+        r->ext[last] *= e;
+        continue;
+      }
+    }
+    r->ext[r->n] = e;
+    r->is[r->n] = s;
+    r->os[r->n] = o;
+    ++r->n;
+  }
+}
+
+// Element types the sideways pass-1 mappings serve (real and integer; complex
+// keeps the plane mapping).
+T4A_HD bool sideways_dtype(int dtype) {
+  return dtype == T4A_CUDA_F32 || dtype == T4A_CUDA_F64 || dtype == T4A_CUDA_I32 ||
+         dtype == T4A_CUDA_I64;
+}
+
+// Pass-1 work mapping (t4a_cuda_reduce_partials). All three keep the
+// reference's per-plane topology; they differ only in which hardware lanes hold
+// which plane lanes:
+//   PLANE      one 32-lane half-wavefront per (output, split) cube, as the
+//              reference warp (any width 8/16/32);
+//   COLUMNS    a strided axis whose fastest non-axis dim (input stride 1) has
+//              at least 64 columns: one lane per column, holding all 32 plane
+//              lanes of that column's cube in registers, so every load of the
+//              wavefront reads 64 adjacent columns of one row;
+//   ROWS       the same with 2..32 columns (a power of two): 64 / C rows per
+//              load, each lane holding the 32 / (64 / C) plane lanes of its
+//              row residue.
+// COLUMNS and ROWS need 32-lane planes and blocks made of whole wavefronts.
+enum PartialsMode { kPartialsPlane = 0, kPartialsColumns = 1, kPartialsRows = 2 };
+
+struct PartialsPlan {
+  int mode;
+  ReduceDims dims;
+  int col_dim;          // fused dim of input stride 1 (COLUMNS/ROWS)
+  long long columns;    // its extent
+  long long col_blocks; // 64-column blocks (COLUMNS), 1 (ROWS)
+  long long others;     // product of the other fused extents
+  long long units;      // wavefront work items (COLUMNS/ROWS) or cubes (PLANE)
+};
+
+T4A_HD void partials_plan(PartialsPlan* p, const t4a_cuda_layout& partials,
+                          const t4a_cuda_layout& in, int axis, long long output_len,
+                          long long splits, int plane_width, int whole_waves) {
+  reduce_dims(&p->dims, partials, in, axis);
+  p->mode = kPartialsPlane;
+  p->col_dim = -1;
+  p->columns = 0;
+  p->col_blocks = 0;
+  p->others = 0;
+  p->units = output_len * splits;
+  if (plane_width != kWarp || !whole_waves || p->dims.axis_stride == 1 || output_len <= 0)
+    return;
+  int col = -1;
+  for (int k = 0; k < p->dims.n; ++k) {
+    if (p->dims.is[k] == 1) col = k;
+  }
+  if (col < 0) return;
+  const long long c = p->dims.ext[col];
+  long long others = 1;
+  for (int k = 0; k < p->dims.n; ++k) {
+    if (k != col) others *= p->dims.ext[k];
+  }
+  if (c >= kWave) {
+    p->mode = kPartialsColumns;
+    p->col_blocks = (c + kWave - 1) / kWave;
+  } else if (c >= 2 && (c & (c - 1)) == 0) {
+    p->mode = kPartialsRows;
+    p->col_blocks = 1;
+  } else {
+    return;
+  }
+  p->col_dim = col;
+  p->columns = c;
+  p->others = others;
+  p->units = p->col_blocks * others * splits;
+}
+
+}  // namespace t4a
+
+#endif  // T4A_GEOMETRY_H_

@@ -1,0 +1,474 @@
+// gfx950 movement kernels: tiled transpose, materialize_strided and
+// strided_to_strided, exported under the reference entry names and argument
+// lists (reference cuda/src/movement.cu:535-610).
+//
+// Movement is a bijection of logical coordinates, so every kernel here copies
+// each element's bits exactly once and the work order is free. The MI355X
+// design: elements are moved as raw 1/4/8/16-byte payloads; both sides of a
+// permute are made contiguous by staging an LA x LB tile through LDS (read along
+// the source-contiguous run, written along the destination-contiguous run) with
+// 16-byte vector accesses where alignment allows; tiles are walked with
+// grid-stride loops, so a block plans once and then streams tiles.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "device.h"
+#include "geometry.h"
+#include "t4a/t4a.h"
+
+namespace t4a {
+namespace {
+
+// One LDS arena per block, shared by every payload width's instantiation.
+// Index tables (2 x 64 offsets) plus the largest tile: 64 x 65 payloads of 8
+// bytes, or 64 x 33 of 16 bytes.
+constexpr int kMoveLdsBytes = 128 * 8 + 64 * 33 * 16;
+constexpr int kTransposeLdsBytes = 64 * 33 * 16;
+
+// V payloads moved as one access: a 16-byte vector when V > 1, else the
+// payload at its own alignment (a c64 element is only 8-byte aligned).
+template <typename P, int V>
+struct alignas(V > 1 ? sizeof(P) * V : alignof(P)) Vec {
+  P v[V];
+};
+
+// ---- tiled transpose ---------------------------------------------------------------
+
+// dst[b*S + i + j*M] = src[src_offset + b*S + i*N + j] for the batch of
+// blockIdx.z. Tile (i-tile fastest, then j-tile) loops stride over gridDim.x.
+// VL / VS: elements per load / store (a 16-byte vector, or 1).
+template <typename P, int VL, int VS>
+__device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __restrict__ src,
+                                                long long src_offset, long long S, long long M,
+                                                long long N, unsigned char* lds) {
+  constexpr int TM = 64;
+  constexpr int TN = sizeof(P) >= 16 ? 32 : 64;
+  constexpr int PITCH = TN + 1;
+  P* tile = reinterpret_cast<P*>(lds);
+  const long long tiles_m = (M + TM - 1) / TM;
+  const long long tiles_n = (N + TN - 1) / TN;
+  const long long per_batch = tiles_m * tiles_n;
+  const long long b = blockIdx.z;
+  const P* s = src + src_offset + b * S;
+  P* d = dst + b * S;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  for (long long t = blockIdx.x; t < per_batch; t += gridDim.x) {
+    const long long i0 = (t % tiles_m) * TM;
+    const long long j0 = (t / tiles_m) * TN;
+    const int rows = static_cast<int>(M - i0 < TM ? M - i0 : TM);
+    const int cols = static_cast<int>(N - j0 < TN ? N - j0 : TN);
+    // Source rows: runs of TN along j. VL divides N and src_offset, so a vector
+    // is wholly inside or wholly past the matrix edge.
+    for (int e = tid; e < TM * (TN / VL); e += nthreads) {
+      const int i = e / (TN / VL);
+      const int j = (e % (TN / VL)) * VL;
+      if (i < rows && j < cols) {
+        const Vec<P, VL> x = *reinterpret_cast<const Vec<P, VL>*>(s + (i0 + i) * N + j0 + j);
+#pragma unroll
+        for (int k = 0; k < VL; ++k) tile[i * PITCH + j + k] = x.v[k];
+      }
+    }
+    __syncthreads();
+    // Destination rows: runs of TM along i.
+    for (int e = tid; e < TN * (TM / VS); e += nthreads) {
+      const int j = e / (TM / VS);
+      const int i = (e % (TM / VS)) * VS;
+      if (i < rows && j < cols) {
+        Vec<P, VS> x;
+#pragma unroll
+        for (int k = 0; k < VS; ++k) x.v[k] = tile[(i + k) * PITCH + j];
+        *reinterpret_cast<Vec<P, VS>*>(d + (j0 + j) * M + i0 + i) = x;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename P>
+__device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
+                                                   long long src_offset, long long S,
+                                                   long long M, long long N,
+                                                   unsigned char* lds) {
+  constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
+  const bool vl = V > 1 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && N % V == 0 &&
+                  src_offset % V == 0;
+  const bool vs = V > 1 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 && M % V == 0;
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  if (vl && vs) {
+    transpose_tiles<P, V, V>(d, s, src_offset, S, M, N, lds);
+  } else if (vl) {
+    transpose_tiles<P, V, 1>(d, s, src_offset, S, M, N, lds);
+  } else if (vs) {
+    transpose_tiles<P, 1, V>(d, s, src_offset, S, M, N, lds);
+  } else {
+    transpose_tiles<P, 1, 1>(d, s, src_offset, S, M, N, lds);
+  }
+}
+
+__device__ __forceinline__ bool transpose_config_valid(const t4a_cuda_transpose_config& c) {
+  const bool tile = c.tile == 8 || c.tile == 16 || c.tile == 32;
+  const bool rows = c.block_rows == 4 || c.block_rows == 8 || c.block_rows == 16;
+  const bool pad = c.padding == 0 || c.padding == 1;
+  const bool vw = c.vector_width == 1 || c.vector_width == 2 || c.vector_width == 4;
+  return tile && rows && pad && vw && c.tile % c.vector_width == 0;
+}
+
+// ---- strided movement --------------------------------------------------------------
+
+// TILED: an la x lb tile; element (i, j) sits at src_base + src_a[i] + j and at
+// dst_base + i + dst_b[j]. VL / VS as above.
+template <typename P, int VL, int VS>
+__device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restrict__ src,
+                                           const MovePlan& p, const long long* src_a,
+                                           const long long* dst_b, P* tile) {
+  const int la = static_cast<int>(p.la);
+  const int lb = static_cast<int>(p.lb);
+  const int pitch = lb + 1;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int a_last = p.a_dims[p.na - 1];
+  const int b_last = p.b_dims[p.nb - 1];
+  for (long long t = blockIdx.x; t < p.tiles; t += gridDim.x) {
+    long long rest = t;
+    const long long ta = rest % p.a_tiles;
+    rest /= p.a_tiles;
+    const long long tb = rest % p.b_tiles;
+    rest /= p.b_tiles;
+    long long sbase = p.src_offset + ta * p.a_tile * p.ss[a_last] + tb * p.b_tile * p.ss[b_last];
+    long long dbase = p.dst_offset + ta * p.a_tile * p.ds[a_last] + tb * p.b_tile * p.ds[b_last];
+    for (int q = 0; q < p.nbatch; ++q) {
+      const int k = p.batch_dims[q];
+      const long long c = rest % p.ext[k];
+      rest /= p.ext[k];
+      sbase += c * p.ss[k];
+      dbase += c * p.ds[k];
+    }
+    const long long a_left = p.ext[a_last] - ta * p.a_tile;
+    const long long b_left = p.ext[b_last] - tb * p.b_tile;
+    const int va = static_cast<int>(p.a_inner * (a_left < p.a_tile ? a_left : p.a_tile));
+    const int vb = static_cast<int>(p.b_inner * (b_left < p.b_tile ? b_left : p.b_tile));
+    const P* s = src + sbase;
+    P* d = dst + dbase;
+    const int lbv = lb / VL;
+    for (int e = tid; e < la * lbv; e += nthreads) {
+      const int i = e / lbv;
+      const int j = (e - i * lbv) * VL;
+      if (i < va && j < vb) {
+        const Vec<P, VL> x = *reinterpret_cast<const Vec<P, VL>*>(s + src_a[i] + j);
+#pragma unroll
+        for (int k = 0; k < VL; ++k) tile[i * pitch + j + k] = x.v[k];
+      }
+    }
+    __syncthreads();
+    const int lav = la / VS;
+    for (int e = tid; e < lb * lav; e += nthreads) {
+      const int j = e / lav;
+      const int i = (e - j * lav) * VS;
+      if (i < va && j < vb) {
+        Vec<P, VS> x;
+#pragma unroll
+        for (int k = 0; k < VS; ++k) x.v[k] = tile[(i + k) * pitch + j];
+        *reinterpret_cast<Vec<P, VS>*>(d + i + dst_b[j]) = x;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Offsets of run position `i` along a chain: mixed-radix digits over the
+// chain's extents (the last digit bounded by the tile), times the other side's
+// strides.
+__device__ __forceinline__ long long chain_offset(const MovePlan& p, const int* dims, int count,
+                                                  long long last_tile, const long long* strides,
+                                                  long long i) {
+  long long off = 0;
+  for (int c = 0; c < count; ++c) {
+    const int k = dims[c];
+    const long long e = c + 1 < count ? p.ext[k] : last_tile;
+    off += (i % e) * strides[k];
+    i /= e;
+  }
+  return off;
+}
+
+// 16-byte accesses along a run need every run start to be a multiple of V:
+// the base offset, every stride outside the run, the tile step of the run's
+// tiled dim, and every partial tile's valid length.
+__device__ __forceinline__ bool run_vectorizable(const MovePlan& p, const int* dims, int count,
+                                                 long long inner, long long tile,
+                                                 const long long* strides, long long offset,
+                                                 int v, const void* ptr) {
+  if (v <= 1 || (reinterpret_cast<uintptr_t>(ptr) & 15) != 0) return false;
+  if (offset % v != 0) return false;
+  const int last = dims[count - 1];
+  const bool tail_ok = inner % v == 0 || (tile % v == 0 && p.ext[last] % v == 0);
+  if (!tail_ok) return false;
+  if ((tile * inner) % v != 0) return false;
+  for (int k = 0; k < p.n; ++k) {
+    if (move_chain_contains(dims, count, k)) continue;
+    if (strides[k] % v != 0) return false;
+  }
+  return true;
+}
+
+template <typename P>
+__device__ __forceinline__ void move_tiled(void* dst, const void* src, const MovePlan& p,
+                                           unsigned char* lds) {
+  long long* src_a = reinterpret_cast<long long*>(lds);
+  long long* dst_b = src_a + 64;
+  P* tile = reinterpret_cast<P*>(lds + 128 * sizeof(long long));
+  for (int i = threadIdx.x; i < p.la; i += blockDim.x)
+    src_a[i] = chain_offset(p, p.a_dims, p.na, p.a_tile, p.ss, i);
+  for (int j = threadIdx.x; j < p.lb; j += blockDim.x)
+    dst_b[j] = chain_offset(p, p.b_dims, p.nb, p.b_tile, p.ds, j);
+  __syncthreads();
+  constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
+  const bool vl = run_vectorizable(p, p.b_dims, p.nb, p.b_inner, p.b_tile, p.ss, p.src_offset,
+                                   V, src);
+  const bool vs = run_vectorizable(p, p.a_dims, p.na, p.a_inner, p.a_tile, p.ds, p.dst_offset,
+                                   V, dst);
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  if (vl && vs) {
+    move_tiles<P, V, V>(d, s, p, src_a, dst_b, tile);
+  } else if (vl) {
+    move_tiles<P, V, 1>(d, s, p, src_a, dst_b, tile);
+  } else if (vs) {
+    move_tiles<P, 1, V>(d, s, p, src_a, dst_b, tile);
+  } else {
+    move_tiles<P, 1, 1>(d, s, p, src_a, dst_b, tile);
+  }
+}
+
+// CONTIG: rows along the fused dim `row_dim`, contiguous on both sides.
+template <typename P>
+__device__ __forceinline__ void move_rows(void* dst, const void* src, const MovePlan& p) {
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < p.len;
+       f += gstride) {
+    long long rest = f / p.row_len;
+    long long so = p.src_offset + (f - rest * p.row_len);
+    long long dof = p.dst_offset + (f - rest * p.row_len);
+    for (int k = 0; k < p.n; ++k) {
+      if (k == p.row_dim) continue;
+      const long long c = rest % p.ext[k];
+      rest /= p.ext[k];
+      so += c * p.ss[k];
+      dof += c * p.ds[k];
+    }
+    d[dof] = s[so];
+  }
+}
+
+// GENERIC: one decode per element on both sides.
+template <typename P>
+__device__ __forceinline__ void move_elements(void* dst, const void* src, const MovePlan& p) {
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < p.len;
+       f += gstride) {
+    long long rest = f;
+    long long so = p.src_offset;
+    long long dof = p.dst_offset;
+    for (int k = 0; k < p.n; ++k) {
+      const long long c = rest % p.ext[k];
+      rest /= p.ext[k];
+      so += c * p.ss[k];
+      dof += c * p.ds[k];
+    }
+    d[dof] = s[so];
+  }
+}
+
+template <typename P>
+__device__ __forceinline__ void move_dispatch(void* dst, const void* src, const MovePlan& p,
+                                              unsigned char* lds) {
+  switch (p.mode) {
+    case kMoveTiled: move_tiled<P>(dst, src, p, lds); break;
+    case kMoveContig: move_rows<P>(dst, src, p); break;
+    case kMoveGeneric: move_elements<P>(dst, src, p); break;
+    default: break;
+  }
+}
+
+__device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype,
+                                           const t4a_cuda_layout& src_layout,
+                                           const long long* dst_strides, long long dst_offset,
+                                           long long len) {
+  const int es = dtype_size(dtype);
+  if (es == 0) return;  // unknown tag: no work (reference c-kernel-abi.md:107-108)
+  __shared__ MovePlan plan;
+  __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
+  if (threadIdx.x == 0) move_plan(&plan, src_layout, dst_strides, dst_offset, len, es);
+  __syncthreads();
+  switch (es) {
+    case 1: move_dispatch<uint8_t>(dst, src, plan, lds); break;
+    case 4: move_dispatch<uint32_t>(dst, src, plan, lds); break;
+    case 8: move_dispatch<unsigned long long>(dst, src, plan, lds); break;
+    case 16: move_dispatch<Elem16>(dst, src, plan, lds); break;
+    default: break;
+  }
+}
+
+// ---- kernels the launchers use: one per payload width, the plan computed on
+// the host and passed by value. ----
+
+template <typename P>
+__global__ void __launch_bounds__(256)
+    transpose_kernel(void* dst, const void* src, long long src_offset, long long batch_stride,
+                     long long dst_fast_extent, long long src_fast_extent) {
+  __shared__ alignas(16) unsigned char lds[kTransposeLdsBytes];
+  transpose_dispatch<P>(dst, src, src_offset, batch_stride, dst_fast_extent, src_fast_extent,
+                        lds);
+}
+
+template <typename P>
+__global__ void __launch_bounds__(256) move_kernel(void* dst, const void* src, MovePlan plan) {
+  __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
+  move_dispatch<P>(dst, src, plan, lds);
+}
+
+}  // namespace
+}  // namespace t4a
+
+using t4a::kBlock;
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_tiled_transpose(void* dst, const void* src, int dtype, long long src_offset,
+                             long long batch_stride, long long dst_fast_extent,
+                             long long src_fast_extent, t4a_cuda_transpose_config config) {
+  // An unsupported configuration or dtype performs no work, as in the reference
+  // (movement.cu:264-266); the MI355X tile does not depend on the config.
+  if (!t4a::transpose_config_valid(config)) return;
+  __shared__ alignas(16) unsigned char lds[t4a::kTransposeLdsBytes];
+  switch (t4a::dtype_size(dtype)) {
+    case 1:
+      t4a::transpose_dispatch<uint8_t>(dst, src, src_offset, batch_stride, dst_fast_extent,
+                                       src_fast_extent, lds);
+      break;
+    case 4:
+      t4a::transpose_dispatch<uint32_t>(dst, src, src_offset, batch_stride, dst_fast_extent,
+                                        src_fast_extent, lds);
+      break;
+    case 8:
+      t4a::transpose_dispatch<unsigned long long>(dst, src, src_offset, batch_stride,
+                                                  dst_fast_extent, src_fast_extent, lds);
+      break;
+    case 16:
+      t4a::transpose_dispatch<t4a::Elem16>(dst, src, src_offset, batch_stride, dst_fast_extent,
+                                           src_fast_extent, lds);
+      break;
+    default:
+      break;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_materialize_strided(void* dst, const void* src, int dtype,
+                                 t4a_cuda_layout src_layout, long long len) {
+  t4a::move_entry(dst, src, dtype, src_layout, nullptr, 0, len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_strided_to_strided(void* dst, const void* src, int dtype,
+                                t4a_cuda_layout src_layout, t4a_cuda_layout dst_layout,
+                                long long len) {
+  // Both layouts share the source's extents (reference movement.cu:139-141).
+  t4a::move_entry(dst, src, dtype, src_layout, dst_layout.strides, dst_layout.offset, len);
+}
+
+// ---- launchers -----------------------------------------------------------------------
+
+namespace {
+
+bool launch_empty(const t4a_launch* l) {
+  return l->grid[0] == 0 || l->grid[1] == 0 || l->grid[2] == 0;
+}
+
+int status_of_last_launch() {
+  return hipGetLastError() == hipSuccess ? T4A_OK : T4A_HIP_ERR_LAUNCH;
+}
+
+template <typename Fn>
+int with_payload(int dtype, Fn&& fn) {
+  switch (t4a::dtype_size(dtype)) {
+    case 1: return fn(static_cast<uint8_t*>(nullptr));
+    case 4: return fn(static_cast<uint32_t*>(nullptr));
+    case 8: return fn(static_cast<unsigned long long*>(nullptr));
+    case 16: return fn(static_cast<t4a::Elem16*>(nullptr));
+    default: return T4A_OK;  // unknown tag: no work, as the reference entry
+  }
+}
+
+bool config_valid(const t4a_cuda_transpose_config& c) {
+  t4a_cuda_transpose_config checked;
+  return t4a_transpose_config_new(c.tile, c.block_rows, c.padding, c.vector_width, &checked) ==
+         T4A_OK;
+}
+
+int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
+                const t4a_launch* launch, void* stream, int dtype) {
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_payload(dtype, [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    hipLaunchKernelGGL(t4a::move_kernel<P>, grid, block, 0, static_cast<hipStream_t>(stream),
+                       dst, src, plan);
+    return status_of_last_launch();
+  });
+}
+
+}  // namespace
+
+extern "C" int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype,
+                                       long long src_offset, long long batch_stride,
+                                       long long dst_fast_extent, long long src_fast_extent,
+                                       t4a_cuda_transpose_config config,
+                                       const t4a_launch* launch, void* stream) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  // An unsupported configuration performs no work (reference movement.cu:264-266).
+  if (!config_valid(config)) return T4A_OK;
+  // The batch index is the grid's z coordinate, as in the reference launch.
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_payload(dtype, [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    hipLaunchKernelGGL(t4a::transpose_kernel<P>, grid, block, 0,
+                       static_cast<hipStream_t>(stream), dst, src, src_offset, batch_stride,
+                       dst_fast_extent, src_fast_extent);
+    return status_of_last_launch();
+  });
+}
+
+extern "C" int t4a_hip_materialize_strided(void* dst, const void* src, int dtype,
+                                           const t4a_cuda_layout* src_layout, long long len,
+                                           const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || src_layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  t4a::MovePlan plan;
+  t4a::move_plan(&plan, *src_layout, nullptr, 0, len, t4a::dtype_size(dtype));
+  return launch_move(dst, src, plan, launch, stream, dtype);
+}
+
+extern "C" int t4a_hip_strided_to_strided(void* dst, const void* src, int dtype,
+                                          const t4a_cuda_layout* src_layout,
+                                          const t4a_cuda_layout* dst_layout, long long len,
+                                          const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || src_layout == nullptr || dst_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  t4a::MovePlan plan;
+  t4a::move_plan(&plan, *src_layout, dst_layout->strides, dst_layout->offset, len,
+                 t4a::dtype_size(dtype));
+  return launch_move(dst, src, plan, launch, stream, dtype);
+}

@@ -1,0 +1,558 @@
+// Checked host planning of the movement and reduction entries.
+//
+// Validation restates the reference planner (src/lib.rs) step for step, so the
+// same bad input is refused with the same Error; each function cites the
+// reference function it follows. The returned geometry is this library's own
+// (MI355X wavefront-sized blocks, work decomposed by geometry.h), except where
+// the geometry carries the fold topology: a PLANE reduction's block width is its
+// plane width, and a pass-1 block of at most 32 threads is one plane of that
+// width, exactly as in the reference (docs/abi/c-kernel-abi.md:291-312).
+#include <climits>
+#include <cstdint>
+#include <cstring>
+
+#include "geometry.h"
+#include "t4a/t4a.h"
+
+namespace {
+
+using t4a::kBlock;
+
+// Reference constants (src/lib.rs:139-150, 3031-3063).
+constexpr unsigned kFlatBlock = 256;
+constexpr unsigned kMaxGridYZ = 65535;
+constexpr unsigned kMaxGridX = INT32_MAX;
+constexpr uint64_t kDefaultSharedBytes = 48 * 1024;
+constexpr long long kMinChunkPlanes = 8;
+constexpr long long kMaxSplits = 4096;
+constexpr unsigned kMaxBlockWidth = 512;
+constexpr long long kWideCombineMinSplits = 64;
+constexpr long long kCombineTargetFoldsPerLane = 8;
+// Grid-stride kernels stop growing the grid here: 1024 blocks per CU.
+constexpr long long kMaxBlocks = 262144;
+
+int ok() { return T4A_OK; }
+
+bool checked_mul(long long a, long long b, long long* out) {
+  return !__builtin_mul_overflow(a, b, out);
+}
+bool checked_add(long long a, long long b, long long* out) {
+  return !__builtin_add_overflow(a, b, out);
+}
+
+// Reference LayoutRef::new / Layout::new validation (src/lib.rs:342-360, 908-928).
+int check_layout(const t4a_cuda_layout* l) {
+  if (l == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (l->rank < 0 || l->rank > T4A_CUDA_MAX_RANK) return T4A_ERR_RANK_OUT_OF_RANGE;
+  for (int k = 0; k < l->rank; ++k) {
+    if (l->extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
+  }
+  return T4A_OK;
+}
+
+// Reference element_count (src/lib.rs:392-397).
+int element_count(const t4a_cuda_layout* l, long long* count) {
+  long long acc = 1;
+  for (int k = 0; k < l->rank; ++k) {
+    if (!checked_mul(acc, l->extents[k], &acc)) return T4A_ERR_OVERFLOW;
+  }
+  *count = acc;
+  return T4A_OK;
+}
+
+// Reference reachable_offset (src/lib.rs:409-422).
+int reachable_offset(const t4a_cuda_layout* l, bool maximum, long long* out) {
+  long long total = l->offset;
+  for (int k = 0; k < l->rank; ++k) {
+    long long step;
+    if (!checked_mul(l->extents[k] - 1, l->strides[k], &step)) return T4A_ERR_OVERFLOW;
+    step = maximum ? (step > 0 ? step : 0) : (step < 0 ? step : 0);
+    if (!checked_add(total, step, &total)) return T4A_ERR_OVERFLOW;
+  }
+  *out = total;
+  return T4A_OK;
+}
+
+// Reference LayoutRef::check_span (src/lib.rs:1011-1027).
+int check_span(const t4a_cuda_layout* l, long long len, int esize) {
+  if (len < 0) return T4A_ERR_NEGATIVE_COUNT;
+  long long count;
+  if (int s = element_count(l, &count)) return s;
+  if (count == 0) return ok();
+  long long lo, hi, bytes;
+  if (int s = reachable_offset(l, false, &lo)) return s;
+  if (int s = reachable_offset(l, true, &hi)) return s;
+  if (lo < 0 || hi >= len) return T4A_ERR_OFFSET_OUT_OF_SPAN;
+  if (!checked_mul(hi, esize, &bytes)) return T4A_ERR_OVERFLOW;
+  return ok();
+}
+
+// Reference require_destination / rejects_broadcast_axis (src/lib.rs:4057-4065, 444-449).
+int require_destination(const t4a_cuda_layout* l) {
+  for (int k = 0; k < l->rank; ++k) {
+    if (l->extents[k] > 1 && l->strides[k] == 0) return T4A_ERR_BROADCAST_DESTINATION;
+  }
+  return ok();
+}
+
+// Reference is_compact (src/lib.rs:425-441).
+bool is_compact(const t4a_cuda_layout* l) {
+  if (l->offset != 0) return false;
+  long long stride = 1;
+  for (int k = 0; k < l->rank; ++k) {
+    if (l->strides[k] != stride) return false;
+    if (!checked_mul(stride, l->extents[k], &stride)) return false;
+  }
+  return true;
+}
+
+bool dtype_known(int dtype) { return t4a::dtype_size(dtype) != 0; }
+
+void set_launch(t4a_launch* out, long long grid, unsigned block, unsigned shared) {
+  out->grid[0] = static_cast<unsigned>(grid);
+  out->grid[1] = grid > 0 ? 1u : 0u;
+  out->grid[2] = grid > 0 ? 1u : 0u;
+  out->block[0] = block;
+  out->block[1] = 1;
+  out->block[2] = 1;
+  out->shared_bytes = shared;
+  out->variant = T4A_VARIANT_FAST;
+}
+
+long long blocks_for(long long items, long long per_block) {
+  long long blocks = (items + per_block - 1) / per_block;
+  return blocks < kMaxBlocks ? blocks : kMaxBlocks;
+}
+
+// Reference flat_launch (src/lib.rs:1465-1482): its refusals are kept; the
+// geometry is this library's.
+int flat_launch_check(long long len) {
+  if (len < 0) return T4A_ERR_NEGATIVE_COUNT;
+  if (len == 0) return ok();
+  const unsigned long long blocks = (static_cast<unsigned long long>(len) + kFlatBlock - 1) /
+                                    kFlatBlock;
+  if (blocks > kMaxGridX) return T4A_ERR_LAUNCH_LIMIT;
+  return ok();
+}
+
+void movement_launch(const t4a::MovePlan& plan, t4a_launch* out) {
+  long long blocks = 0;
+  switch (plan.mode) {
+    case t4a::kMoveTiled: blocks = blocks_for(plan.tiles, 1); break;
+    case t4a::kMoveContig: blocks = blocks_for(plan.len, kBlock * 4); break;
+    case t4a::kMoveGeneric: blocks = blocks_for(plan.len, kBlock * 4); break;
+    default: blocks = 0; break;
+  }
+  set_launch(out, blocks, kBlock, 0);
+}
+
+// ---- reductions ----
+
+bool op_supports(int op, int dtype) {
+  switch (op) {
+    case T4A_CUDA_REDUCE_SUM:
+    case T4A_CUDA_REDUCE_PROD:
+      return dtype == T4A_CUDA_F32 || dtype == T4A_CUDA_F64 || dtype == T4A_CUDA_I32 ||
+             dtype == T4A_CUDA_I64 || dtype == T4A_CUDA_C32 || dtype == T4A_CUDA_C64;
+    case T4A_CUDA_REDUCE_SUM_SQUARES:
+      return dtype == T4A_CUDA_F32 || dtype == T4A_CUDA_F64;
+    case T4A_CUDA_REDUCE_MAX:
+    case T4A_CUDA_REDUCE_MIN:
+      return dtype == T4A_CUDA_F32 || dtype == T4A_CUDA_F64 || dtype == T4A_CUDA_I32 ||
+             dtype == T4A_CUDA_I64;
+    default:
+      return false;
+  }
+}
+
+bool plane_width_ok(unsigned w) { return w == 8 || w == 16 || w == 32; }
+bool combine_width_ok(unsigned w) { return w == 64 || w == 128 || w == 256 || w == 512; }
+
+// Reference reduce_problem (src/lib.rs:3193-3233).
+int reduce_problem(int dtype, int op, const t4a_cuda_layout* out, long long out_len,
+                   const t4a_cuda_layout* in, long long in_len, unsigned axis,
+                   long long* reduce_len, long long* output_len) {
+  if (!op_supports(op, dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (axis >= static_cast<unsigned>(in->rank)) return T4A_ERR_INVALID_AXIS;
+  if (out->rank != in->rank) return T4A_ERR_RANK_LENGTH;
+  for (int k = 0; k < in->rank; ++k) {
+    if (static_cast<unsigned>(k) == axis) continue;
+    if (out->extents[k] != in->extents[k]) return T4A_ERR_SHAPE_MISMATCH;
+  }
+  if (out->extents[axis] != 1) return T4A_ERR_SHAPE_MISMATCH;
+  *reduce_len = in->extents[axis];
+  if (*reduce_len < 1) return T4A_ERR_NEGATIVE_COUNT;
+  if (int s = element_count(out, output_len)) return s;
+  if (int s = require_destination(out)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(in, in_len, es)) return s;
+  if (int s = check_span(out, out_len, es)) return s;
+  return ok();
+}
+
+int strategy_for(long long reduce_len, unsigned w) {
+  return reduce_len <= static_cast<long long>(w) ? T4A_CUDA_REDUCE_UNIT : T4A_CUDA_REDUCE_PLANE;
+}
+
+// Reference launch_for (src/lib.rs:3243-3286), with this library's UNIT geometry:
+// a unit reduction's fold does not depend on the block, so it runs 256-thread
+// blocks; a PLANE block is the plane.
+int launch_for(int strategy, long long output_len, unsigned w, t4a_launch* out) {
+  if (strategy == T4A_CUDA_REDUCE_UNIT) {
+    if (output_len < 0) return T4A_ERR_NEGATIVE_COUNT;
+    const unsigned long long blocks =
+        (static_cast<unsigned long long>(output_len) + w - 1) / w;
+    if (blocks > UINT32_MAX) return T4A_ERR_LAUNCH_LIMIT;
+    if (blocks > kMaxGridX) return T4A_ERR_LAUNCH_LIMIT;
+    set_launch(out, output_len == 0 ? 0 : blocks_for(output_len, kBlock), kBlock, 0);
+    return ok();
+  }
+  if (output_len < 0 || output_len > static_cast<long long>(UINT32_MAX))
+    return T4A_ERR_LAUNCH_LIMIT;
+  if (static_cast<unsigned long long>(output_len) > kMaxGridX) return T4A_ERR_LAUNCH_LIMIT;
+  set_launch(out, output_len, w, 0);
+  if (output_len == 0) out->grid[1] = out->grid[2] = 1;
+  return ok();
+}
+
+int combine_block_width(long long splits) {
+  const long long target = splits / kCombineTargetFoldsPerLane;
+  unsigned width = static_cast<unsigned>(kWideCombineMinSplits);
+  while (static_cast<long long>(width) < target && width < kMaxBlockWidth) width *= 2;
+  return width < kMaxBlockWidth ? width : kMaxBlockWidth;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t4a_abi_revision(void) { return T4A_CUDA_ABI_REVISION; }
+
+int t4a_dtype_size(int dtype) { return t4a::dtype_size(dtype); }
+
+const char* t4a_status_name(int status) {
+  static const char* const names[] = {
+      "Ok",                 "RankOutOfRange",    "RankLength",
+      "NegativeExtent",     "NegativeCount",     "Overflow",
+      "CountMismatch",      "OffsetOutOfSpan",   "BroadcastDestination",
+      "UnsupportedDType",   "NotElementwise",    "LaunchLimit",
+      "InvalidTransposeConfig", "InvalidAxis",   "DuplicateAxis",
+      "NotCompact",         "ShapeMismatch",     "InvalidStep",
+      "InvalidPadding",     "DomainTooLarge",    "InvalidStride",
+      "StrategyMismatch",   "InvalidPlaneWidth", "InvalidSplit",
+      "IndexVectorMismatch", "UnsupportedOp"};
+  if (status >= 0 && status < static_cast<int>(sizeof(names) / sizeof(names[0])))
+    return names[status];
+  if (status == T4A_HIP_ERR_LAUNCH) return "HipLaunch";
+  if (status == T4A_HIP_ERR_NULL_ARGUMENT) return "NullArgument";
+  return "Unknown";
+}
+
+int t4a_layout_new(t4a_cuda_layout* out, int rank, const long long* extents,
+                   const long long* strides, long long offset) {
+  if (out == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (rank < 0 || rank > T4A_CUDA_MAX_RANK) return T4A_ERR_RANK_OUT_OF_RANGE;
+  if (rank > 0 && (extents == nullptr || strides == nullptr)) return T4A_HIP_ERR_NULL_ARGUMENT;
+  for (int k = 0; k < rank; ++k) {
+    if (extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
+  }
+  std::memset(out, 0, sizeof(*out));
+  out->rank = rank;
+  out->offset = offset;
+  for (int k = 0; k < rank; ++k) {
+    out->extents[k] = extents[k];
+    out->strides[k] = strides[k];
+  }
+  return ok();
+}
+
+// Reference Layout::compact (src/lib.rs:362-374).
+int t4a_layout_compact(t4a_cuda_layout* out, int rank, const long long* extents) {
+  if (out == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (rank < 0 || rank > T4A_CUDA_MAX_RANK) return T4A_ERR_RANK_OUT_OF_RANGE;
+  long long strides[T4A_CUDA_MAX_RANK] = {0};
+  long long stride = 1;
+  for (int k = 0; k < rank; ++k) {
+    strides[k] = stride;
+    if (!checked_mul(stride, extents[k], &stride)) return T4A_ERR_OVERFLOW;
+  }
+  return t4a_layout_new(out, rank, extents, strides, 0);
+}
+
+int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count) {
+  if (count == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(layout)) return s;
+  return element_count(layout, count);
+}
+
+// Reference plan_materialize_strided (src/lib.rs:1628-1641).
+int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
+                                 t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(src)) return s;
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  long long len;
+  if (int s = element_count(src, &len)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(src, src_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  t4a::MovePlan plan;
+  t4a::move_plan(&plan, *src, nullptr, 0, len, es);
+  movement_launch(plan, launch);
+  return ok();
+}
+
+// Reference plan_strided_to_strided (src/lib.rs:1660-1679).
+int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
+                                const t4a_cuda_layout* dst, long long dst_len,
+                                t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(src)) return s;
+  if (int s = check_layout(dst)) return s;
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  bool same = src->rank == dst->rank;
+  for (int k = 0; same && k < src->rank; ++k) same = src->extents[k] == dst->extents[k];
+  if (!same) return T4A_ERR_COUNT_MISMATCH;
+  long long len;
+  if (int s = element_count(src, &len)) return s;
+  if (int s = require_destination(dst)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(src, src_len, es)) return s;
+  if (int s = check_span(dst, dst_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  t4a::MovePlan plan;
+  t4a::move_plan(&plan, *src, dst->strides, dst->offset, len, es);
+  movement_launch(plan, launch);
+  return ok();
+}
+
+// Reference TransposeConfig::new (src/lib.rs:471-491).
+int t4a_transpose_config_new(int tile, int block_rows, int padding, int vector_width,
+                             t4a_cuda_transpose_config* config) {
+  if (config == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const bool ok_tile = tile == 8 || tile == 16 || tile == 32;
+  const bool ok_rows = block_rows == 4 || block_rows == 8 || block_rows == 16;
+  const bool ok_pad = padding == 0 || padding == 1;
+  const bool ok_vw = vector_width == 1 || vector_width == 2 || vector_width == 4;
+  if (!ok_tile || !ok_rows || !ok_pad || !ok_vw || tile % vector_width != 0)
+    return T4A_ERR_INVALID_TRANSPOSE_CONFIG;
+  config->tile = tile;
+  config->block_rows = block_rows;
+  config->padding = padding;
+  config->vector_width = vector_width;
+  return ok();
+}
+
+t4a_cuda_transpose_config t4a_transpose_config_default(void) {
+  t4a_cuda_transpose_config c = {16, 8, 1, 1};
+  return c;
+}
+
+// Reference plan_tiled_transpose (src/lib.rs:1681-1737). The config is validated
+// and its shared-memory demand checked exactly as the reference does; the
+// MI355X kernel stages its own 64-element-wide tiles in static LDS, so the
+// returned launch is a 1-D grid of tiles with no dynamic shared memory.
+int t4a_plan_tiled_transpose(int dtype, t4a_cuda_transpose_config config, long long src_offset,
+                             long long batch_stride, long long dst_fast_extent,
+                             long long src_fast_extent, long long batches, long long src_len,
+                             long long dst_len, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  t4a_cuda_transpose_config checked;
+  if (int s = t4a_transpose_config_new(config.tile, config.block_rows, config.padding,
+                                       config.vector_width, &checked))
+    return s;
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (dst_fast_extent < 0 || src_fast_extent < 0 || batches < 0 || src_offset < 0)
+    return T4A_ERR_NEGATIVE_COUNT;
+  long long matrix, span, end;
+  if (!checked_mul(dst_fast_extent, src_fast_extent, &matrix)) return T4A_ERR_OVERFLOW;
+  if (batch_stride != matrix) return T4A_ERR_INVALID_TRANSPOSE_CONFIG;
+  if (!checked_mul(matrix, batches, &span)) return T4A_ERR_OVERFLOW;
+  if (!checked_add(src_offset, span, &end)) return T4A_ERR_OVERFLOW;
+  if (end > src_len || span > dst_len) return T4A_ERR_OFFSET_OUT_OF_SPAN;
+  const int es = t4a::dtype_size(dtype);
+  const uint64_t shared = static_cast<uint64_t>(config.tile) *
+                          static_cast<uint64_t>(config.tile + config.padding) *
+                          static_cast<uint64_t>(es);
+  if (shared > kDefaultSharedBytes) return T4A_ERR_LAUNCH_LIMIT;
+  const unsigned long long gx = (static_cast<unsigned long long>(dst_fast_extent) + config.tile - 1) /
+                                static_cast<unsigned long long>(config.tile);
+  const unsigned long long gy = (static_cast<unsigned long long>(src_fast_extent) + config.tile - 1) /
+                                static_cast<unsigned long long>(config.tile);
+  if (gx > UINT32_MAX || gy > UINT32_MAX) return T4A_ERR_LAUNCH_LIMIT;
+  if (static_cast<unsigned long long>(batches) > UINT32_MAX) return T4A_ERR_LAUNCH_LIMIT;
+  if (gx > kMaxGridX || gy > kMaxGridYZ || static_cast<unsigned long long>(batches) > kMaxGridYZ)
+    return T4A_ERR_LAUNCH_LIMIT;
+  if (gx == 0 || gy == 0 || batches == 0) {
+    set_launch(launch, 0, kBlock, 0);
+    return ok();
+  }
+  // One matrix's tiles stride over x; the batch is the z coordinate, as in the
+  // reference grid (the kernel reads the batch count from nowhere else).
+  const t4a::TransposeTiling tiling = t4a::transpose_tiling(dst_fast_extent, src_fast_extent, 1, es);
+  set_launch(launch, blocks_for(tiling.total, 1), kBlock, 0);
+  launch->grid[2] = static_cast<unsigned>(batches);
+  return ok();
+}
+
+// Reference split_policy (src/lib.rs:3152-3166).
+int t4a_split_policy(long long reduce_len, unsigned int plane_width, int* has_split,
+                     t4a_split* split) {
+  if (has_split == nullptr || split == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  *has_split = 0;
+  split->splits = 0;
+  split->chunk_len = 0;
+  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  if (reduce_len < 1) return ok();
+  const long long min_chunk = static_cast<long long>(plane_width) * kMinChunkPlanes;
+  long long splits = reduce_len / min_chunk;
+  if (splits < 1) splits = 1;
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits <= 1) return ok();
+  *has_split = 1;
+  split->splits = splits;
+  split->chunk_len = reduce_len / splits;
+  return ok();
+}
+
+// Reference plan_reduce (src/lib.rs:3318-3338) with check_reduce_width and
+// check_strategy (3288-3316).
+int t4a_plan_reduce(int dtype, int op, int strategy, const t4a_cuda_layout* out_layout,
+                    long long out_len, const t4a_cuda_layout* in_layout, long long in_len,
+                    unsigned int axis, unsigned int plane_width, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(out_layout)) return s;
+  if (int s = check_layout(in_layout)) return s;
+  if (strategy != T4A_CUDA_REDUCE_UNIT && strategy != T4A_CUDA_REDUCE_PLANE)
+    return T4A_ERR_UNSUPPORTED_OP;
+  if (strategy == T4A_CUDA_REDUCE_UNIT) {
+    if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  } else if (!combine_width_ok(plane_width) && !plane_width_ok(plane_width)) {
+    return T4A_ERR_INVALID_PLANE_WIDTH;
+  }
+  long long reduce_len, output_len;
+  if (int s = reduce_problem(dtype, op, out_layout, out_len, in_layout, in_len, axis,
+                             &reduce_len, &output_len))
+    return s;
+  if (strategy == T4A_CUDA_REDUCE_UNIT && reduce_len > static_cast<long long>(plane_width))
+    return T4A_ERR_STRATEGY_MISMATCH;
+  if (strategy == T4A_CUDA_REDUCE_PLANE && reduce_len < static_cast<long long>(plane_width))
+    return T4A_ERR_STRATEGY_MISMATCH;
+  return launch_for(strategy, output_len, plane_width, launch);
+}
+
+// Reference plan_reduce_partials (src/lib.rs:3340-3431). A 32-lane plan runs
+// 256-thread blocks (eight planes, or four wavefronts of the COLUMNS/ROWS
+// mappings); an 8- or 16-lane plan keeps one plane per block.
+int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_layout,
+                             long long partials_len, const t4a_cuda_layout* in_layout,
+                             long long in_len, unsigned int axis, t4a_split split,
+                             unsigned int plane_width, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(partials_layout)) return s;
+  if (int s = check_layout(in_layout)) return s;
+  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  if (!op_supports(op, dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (axis >= static_cast<unsigned>(in_layout->rank)) return T4A_ERR_INVALID_AXIS;
+  if (partials_layout->rank != in_layout->rank) return T4A_ERR_RANK_LENGTH;
+  for (int k = 0; k < in_layout->rank; ++k) {
+    if (static_cast<unsigned>(k) == axis) continue;
+    if (partials_layout->extents[k] != in_layout->extents[k]) return T4A_ERR_SHAPE_MISMATCH;
+  }
+  const long long reduce_len = in_layout->extents[axis];
+  if (reduce_len < 1) return T4A_ERR_NEGATIVE_COUNT;
+  if (split.splits < 2 || split.chunk_len < static_cast<long long>(plane_width) ||
+      split.chunk_len != reduce_len / split.splits || split.splits > kMaxSplits)
+    return T4A_ERR_INVALID_SPLIT;
+  if (partials_layout->extents[axis] != split.splits) return T4A_ERR_SHAPE_MISMATCH;
+  if (int s = require_destination(partials_layout)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(in_layout, in_len, es)) return s;
+  if (int s = check_span(partials_layout, partials_len, es)) return s;
+  long long output_len = 1;
+  for (int k = 0; k < partials_layout->rank; ++k) {
+    if (static_cast<unsigned>(k) == axis) continue;
+    if (!checked_mul(output_len, partials_layout->extents[k], &output_len))
+      return T4A_ERR_OVERFLOW;
+  }
+  if (output_len < 0) return T4A_ERR_NEGATIVE_COUNT;
+  long long cubes;
+  if (!checked_mul(output_len, split.splits, &cubes)) return T4A_ERR_OVERFLOW;
+  if (cubes > static_cast<long long>(UINT32_MAX)) return T4A_ERR_LAUNCH_LIMIT;
+  if (cubes > static_cast<long long>(kMaxGridX)) return T4A_ERR_LAUNCH_LIMIT;
+  if (plane_width != static_cast<unsigned>(t4a::kWarp)) {
+    set_launch(launch, cubes, plane_width, 0);
+    if (cubes == 0) launch->grid[1] = launch->grid[2] = 1;
+    return ok();
+  }
+  t4a::PartialsPlan plan;
+  t4a::partials_plan(&plan, *partials_layout, *in_layout, static_cast<int>(axis), output_len,
+                     split.splits, t4a::kWarp, t4a::sideways_dtype(dtype));
+  const long long per_block =
+      plan.mode == t4a::kPartialsPlane ? kBlock / t4a::kWarp : kBlock / t4a::kWave;
+  set_launch(launch, plan.units == 0 ? 0 : blocks_for(plan.units, per_block), kBlock, 0);
+  return ok();
+}
+
+// Reference plan_reduction (src/lib.rs:3457-3528) with combine_geometry and
+// combine_block_width (3433-3452).
+int t4a_plan_reduction(int dtype, int op, const t4a_cuda_layout* out_layout, long long out_len,
+                       const t4a_cuda_layout* in_layout, long long in_len, unsigned int axis,
+                       unsigned int plane_width, t4a_reduction_plan* plan) {
+  if (plan == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  std::memset(plan, 0, sizeof(*plan));
+  if (int s = check_layout(out_layout)) return s;
+  if (int s = check_layout(in_layout)) return s;
+  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  long long reduce_len, output_len;
+  if (int s = reduce_problem(dtype, op, out_layout, out_len, in_layout, in_len, axis,
+                             &reduce_len, &output_len))
+    return s;
+  const int strategy = strategy_for(reduce_len, plane_width);
+  int has_split;
+  t4a_split split;
+  if (int s = t4a_split_policy(reduce_len, plane_width, &has_split, &split)) return s;
+  if (!has_split) {
+    plan->kind = T4A_PLAN_DIRECT;
+    plan->strategy = strategy;
+    return t4a_plan_reduce(dtype, op, strategy, out_layout, out_len, in_layout, in_len, axis,
+                           plane_width, &plan->launch);
+  }
+  t4a_cuda_layout partials;
+  if (int s = t4a_reduction_partials_layout(in_layout, axis, split.splits, &partials)) return s;
+  long long partials_len;
+  if (int s = element_count(&partials, &partials_len)) return s;
+  plan->kind = T4A_PLAN_SPLIT;
+  plan->split = split;
+  if (int s = t4a_plan_reduce_partials(dtype, op, &partials, partials_len, in_layout, in_len,
+                                       axis, split, plane_width, &plan->pass1))
+    return s;
+  const int combine_op = op == T4A_CUDA_REDUCE_SUM_SQUARES ? T4A_CUDA_REDUCE_SUM : op;
+  int combine_strategy;
+  unsigned combine_width;
+  if (combine_op == T4A_CUDA_REDUCE_PROD || split.splits < kWideCombineMinSplits) {
+    combine_strategy = strategy_for(split.splits, plane_width);
+    combine_width = plane_width;
+  } else {
+    combine_strategy = T4A_CUDA_REDUCE_PLANE;
+    combine_width = static_cast<unsigned>(combine_block_width(split.splits));
+  }
+  plan->combine_strategy = combine_strategy;
+  plan->combine_op = combine_op;
+  return t4a_plan_reduce(dtype, combine_op, combine_strategy, out_layout, out_len, &partials,
+                         partials_len, axis, combine_width, &plan->pass2);
+}
+
+// Reference reduction_partials_layout / partials_layout_for (src/lib.rs:3530-3557).
+int t4a_reduction_partials_layout(const t4a_cuda_layout* in_layout, unsigned int axis,
+                                  long long splits, t4a_cuda_layout* partials_layout) {
+  if (partials_layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(in_layout)) return s;
+  if (axis >= static_cast<unsigned>(in_layout->rank)) return T4A_ERR_INVALID_AXIS;
+  long long extents[T4A_CUDA_MAX_RANK];
+  for (int k = 0; k < in_layout->rank; ++k) extents[k] = in_layout->extents[k];
+  extents[axis] = splits;
+  return t4a_layout_compact(partials_layout, in_layout->rank, extents);
+}
+
+}  // extern "C"

@@ -1,0 +1,668 @@
+// gfx950 single-axis reductions, exported under the reference entry names and
+// argument lists: t4a_cuda_reduce (unit and plane strategies, narrow and wide
+// plane folds) and t4a_cuda_reduce_partials (pass 1 of a split reduction).
+// Reference: cuda/src/reduce.cu:110-633, 765-852.
+//
+// Every kernel keeps the reference's numerical topology: a unit output folds
+// its axis serially from element 0; a plane lane t seeds element t and folds
+// t + W, t + 2W, ... in order, then the lanes meet in the own-left xor tree; a
+// pass-1 plane takes the grouped 16-byte walk on a contiguous axis and the
+// serial lane walk elsewhere (reference docs/abi/c-kernel-abi.md:313-359). So
+// float results equal the reference kernels' bit for bit wherever IEEE rounding
+// alone decides them.
+//
+// What is MI355X-specific is where the plane lanes live:
+//   - a 32-lane plane is half of a 64-lane wavefront (two cubes per wavefront),
+//     its xor tree a width-32 lane exchange;
+//   - on a strided axis, pass 1 turns the plane sideways: a wavefront lane holds
+//     one output column and all (COLUMNS) or a residue class (ROWS) of its
+//     plane's 32 lanes in registers, so each wavefront load reads 64 adjacent
+//     elements of one or more rows instead of 32 elements a row apart.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "device.h"
+#include "geometry.h"
+#include "t4a/t4a.h"
+
+namespace t4a {
+namespace {
+
+template <typename T>
+struct VecLanes {
+  static constexpr int value = 0;
+};
+template <>
+struct VecLanes<float> {
+  static constexpr int value = 4;
+};
+template <>
+struct VecLanes<double> {
+  static constexpr int value = 2;
+};
+template <>
+struct VecLanes<int> {
+  static constexpr int value = 4;
+};
+template <>
+struct VecLanes<long long> {
+  static constexpr int value = 2;
+};
+
+template <typename T, int V>
+struct alignas(16) Group {
+  T x[V];
+};
+
+// Input base and output offset of output `o` over the fused non-axis dims
+// (reference reduce.cu:110-130); `o` < output_len, so the last dim needs no
+// division.
+// The loop runs over the fixed maximum rank so every field index is a
+// compile-time constant: a runtime subscript would copy the by-value plan into
+// per-lane scratch memory.
+__device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
+                                              long long* in_base, long long* out_off) {
+  long long ib = rd.in_offset;
+  long long ob = rd.out_offset;
+#pragma unroll
+  for (int k = 0; k < kMaxDims; ++k) {
+    if (k >= rd.n) break;
+    long long c;
+    if (k + 1 == rd.n) {
+      c = o;
+    } else {
+      const long long e = rd.ext[k];
+      c = o % e;
+      o /= e;
+    }
+    ib += c * rd.is[k];
+    ob += c * rd.os[k];
+  }
+  *in_base = ib;
+  *out_off = ob;
+}
+
+// ---- t4a_cuda_reduce: UNIT ---------------------------------------------------------
+// One thread per output, serial fold from element 0 (reference reduce.cu:196-224).
+// On a contiguous axis whose every output starts 16-byte aligned, the elements
+// arrive as 16-byte groups; the fold order is unchanged.
+template <typename Fold, typename T, bool Vector>
+__device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __restrict__ in,
+                                             const ReduceDims& rd, long long output_len,
+                                             Fold f) {
+  const long long len = rd.axis_len;
+  const long long stride = rd.axis_stride;
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long o = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+       o < output_len; o += gstride) {
+    long long ib, ob;
+    decode_output(rd, o, &ib, &ob);
+    const T* x = in + ib;
+    T acc;
+    if constexpr (Vector) {
+      constexpr int V = VecLanes<T>::value;
+      const Group<T, V> g0 = *reinterpret_cast<const Group<T, V>*>(x);
+      acc = f.seed(g0.x[0]);
+#pragma unroll
+      for (int c = 1; c < V; ++c) acc = f.fold(acc, g0.x[c]);
+      long long i = V;
+      for (; i + V <= len; i += V) {
+        const Group<T, V> g = *reinterpret_cast<const Group<T, V>*>(x + i);
+#pragma unroll
+        for (int c = 0; c < V; ++c) acc = f.fold(acc, g.x[c]);
+      }
+      for (; i < len; ++i) acc = f.fold(acc, x[i]);
+    } else {
+      acc = f.seed(x[0]);
+#pragma unroll 4
+      for (long long i = 1; i < len; ++i) acc = f.fold(acc, x[i * stride]);
+    }
+    out[ob] = acc;
+  }
+}
+
+template <typename Fold, typename T>
+__device__ __forceinline__ void unit_body(void* out, const void* in, const ReduceDims& rd,
+                                          long long output_len, Fold f) {
+  T* o = static_cast<T*>(out);
+  const T* x = static_cast<const T*>(in);
+  if constexpr (VecLanes<T>::value > 0) {
+    constexpr int V = VecLanes<T>::value;
+    bool vector = rd.axis_stride == 1 && rd.axis_len >= V && rd.in_offset % V == 0 &&
+                  (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+#pragma unroll
+    for (int k = 0; k < kMaxDims; ++k) vector = vector && (k >= rd.n || rd.is[k] % V == 0);
+    if (vector) {
+      unit_outputs<Fold, T, true>(o, x, rd, output_len, f);
+      return;
+    }
+  }
+  unit_outputs<Fold, T, false>(o, x, rd, output_len, f);
+}
+
+// ---- t4a_cuda_reduce: PLANE --------------------------------------------------------
+// One plane of W = blockDim.x lanes per output (reference reduce.cu:226-340).
+// W <= 32: the xor tree. W = 64..512: the xor tree inside each 32-lane warp,
+// warp results through LDS, then warp 0 folds them with the xor tree over the
+// first W / 32 lanes (reference reduce.cu:170-194).
+template <typename Fold, typename T>
+__device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr,
+                                           const ReduceDims& rd, long long output_len, Fold f,
+                                           unsigned char* lds) {
+  T* out = static_cast<T*>(out_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  T* warp_results = reinterpret_cast<T*>(lds);
+  const int w = blockDim.x;
+  const int lane = threadIdx.x;
+  const long long len = rd.axis_len;
+  const long long stride = rd.axis_stride;
+  for (long long o = blockIdx.x; o < output_len; o += gridDim.x) {
+    long long ib, ob;
+    decode_output(rd, o, &ib, &ob);
+    const T* x = in + ib;
+    T acc = f.seed(x[lane * stride]);
+#pragma unroll 4
+    for (long long i = lane + w; i < len; i += w) acc = f.fold(acc, x[i * stride]);
+    T reduced;
+    if (w <= kWarp) {
+      reduced = plane_tree(acc, w, f);
+    } else {
+      acc = plane_tree(acc, kWarp, f);
+      const int warps = w / kWarp;
+      const int wl = lane & (kWarp - 1);
+      const int warp = lane / kWarp;
+      if (wl == 0) warp_results[warp] = acc;
+      __syncthreads();
+      reduced = acc;
+      if (warp == 0) {
+        const T c = wl < warps ? warp_results[wl] : acc;
+        reduced = plane_tree(c, warps, f);
+      }
+      __syncthreads();  // warp_results is reused by the next output
+    }
+    if (lane == 0) out[ob] = reduced;
+  }
+}
+
+// ---- t4a_cuda_reduce_partials -----------------------------------------------------
+
+// Serial lane walk: lane t seeds start + t and folds start + t + kW (reference
+// reduce.cu:349-365).
+template <typename Fold, typename T>
+__device__ __forceinline__ T walk_scalar(const T* __restrict__ in, long long ib,
+                                         long long stride, long long start, long long end,
+                                         int w, int lane, Fold f) {
+  long long r = start + lane;
+  T acc = f.seed(in[ib + r * stride]);
+#pragma unroll 4
+  for (r += w; r < end; r += w) acc = f.fold(acc, in[ib + r * stride]);
+  return acc;
+}
+
+template <typename Fold, typename T, int V>
+__device__ __forceinline__ T group_value(const Group<T, V>& g, Fold f) {
+  if constexpr (V == 4) {
+    return f.combine(f.combine(f.seed(g.x[0]), f.seed(g.x[1])),
+                     f.combine(f.seed(g.x[2]), f.seed(g.x[3])));
+  } else {
+    return f.combine(f.seed(g.x[0]), f.seed(g.x[1]));
+  }
+}
+
+template <typename T, int V, bool Aligned>
+__device__ __forceinline__ Group<T, V> load_group(const T* chunk, long long g) {
+  if constexpr (Aligned) {
+    return reinterpret_cast<const Group<T, V>*>(chunk)[g];
+  } else {
+    Group<T, V> r;
+#pragma unroll
+    for (int c = 0; c < V; ++c) r.x[c] = chunk[g * V + c];
+    return r;
+  }
+}
+
+// Grouped walk of a contiguous chunk (reference reduce.cu:449-525, topology of
+// c-kernel-abi.md:313-359): groups of V elements; lane t takes groups t, t+W,
+// t+2W, ... in batches of four -- the first group seeds, the next three join one
+// at a time, each later whole batch joins as (g0+g1)+(g2+g3), at most three
+// leftovers join one at a time -- then lane t < len mod V folds tail element
+// groups*V + t.
+template <typename Fold, typename T, bool Aligned>
+__device__ __forceinline__ T walk_vector(const T* __restrict__ chunk, long long len, int w,
+                                         int lane, Fold f) {
+  constexpr int V = VecLanes<T>::value;
+  const long long groups = len / V;
+  Group<T, V> b[4];
+  b[0] = load_group<T, V, Aligned>(chunk, lane);
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    if (lane + static_cast<long long>(k) * w < groups)
+      b[k] = load_group<T, V, Aligned>(chunk, lane + static_cast<long long>(k) * w);
+  }
+  T acc = group_value<Fold, T, V>(b[0], f);
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    if (lane + static_cast<long long>(k) * w < groups)
+      acc = f.combine(acc, group_value<Fold, T, V>(b[k], f));
+  }
+  long long idx = lane + 4LL * w;
+  for (; idx + 3LL * w < groups; idx += 4LL * w) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      b[k] = load_group<T, V, Aligned>(chunk, idx + static_cast<long long>(k) * w);
+    const T lo = f.combine(group_value<Fold, T, V>(b[0], f), group_value<Fold, T, V>(b[1], f));
+    const T hi = f.combine(group_value<Fold, T, V>(b[2], f), group_value<Fold, T, V>(b[3], f));
+    acc = f.combine(acc, f.combine(lo, hi));
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (idx + static_cast<long long>(k) * w < groups)
+      b[k] = load_group<T, V, Aligned>(chunk, idx + static_cast<long long>(k) * w);
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (idx + static_cast<long long>(k) * w < groups)
+      acc = f.combine(acc, group_value<Fold, T, V>(b[k], f));
+  }
+  const long long tail = groups * V;
+  if (lane < len - tail) acc = f.fold(acc, chunk[tail + lane]);
+  return acc;
+}
+
+template <typename Fold, typename T>
+__device__ __forceinline__ T pass1_walk(const T* __restrict__ in, long long ib, long long stride,
+                                        long long start, long long end, int w, int lane,
+                                        Fold f) {
+  if constexpr (Fold::kRegroup && VecLanes<T>::value > 0) {
+    constexpr int V = VecLanes<T>::value;
+    // The stride is tested before a chunk pointer is formed: only a contiguous
+    // axis makes in + ib + start an address inside the input.
+    if (stride == 1 && (end - start) / V >= w) {
+      const T* chunk = in + ib + start;
+      if ((reinterpret_cast<uintptr_t>(chunk) & 15) == 0)
+        return walk_vector<Fold, T, true>(chunk, end - start, w, lane, f);
+      return walk_vector<Fold, T, false>(chunk, end - start, w, lane, f);
+    }
+  }
+  return walk_scalar<Fold, T>(in, ib, stride, start, end, w, lane, f);
+}
+
+// PLANE mapping: plane = W lanes (W = blockDim.x when blockDim.x <= 32, else 32
+// with blockDim.x / 32 planes per block, reference reduce.cu:557-581); planes
+// stride over the cubes.
+template <typename Fold, typename T>
+__device__ __forceinline__ void partials_planes(void* partials_ptr, const void* in_ptr,
+                                                const PartialsPlan& pp, long long output_len,
+                                                long long splits, long long chunk_len, Fold f) {
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const int w = blockDim.x <= static_cast<unsigned>(kWarp) ? static_cast<int>(blockDim.x) : kWarp;
+  const int planes = static_cast<int>(blockDim.x) / w;
+  const int lane = static_cast<int>(threadIdx.x) % w;
+  const long long cubes = output_len * splits;
+  const ReduceDims& rd = pp.dims;
+  for (long long cube = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
+       cube < cubes; cube += static_cast<long long>(gridDim.x) * planes) {
+    const long long o = cube / splits;
+    const long long split = cube - o * splits;
+    long long ib, pb;
+    decode_output(rd, o, &ib, &pb);
+    pb += split * rd.out_axis_stride;
+    const long long start = split * chunk_len;
+    const long long end = split + 1 == splits ? rd.axis_len : start + chunk_len;
+    const T acc = pass1_walk<Fold, T>(in, ib, rd.axis_stride, start, end, w, lane, f);
+    const T reduced = plane_tree(acc, w, f);
+    if (lane == 0) partials[pb] = reduced;
+  }
+}
+
+// Unit `u` of the COLUMNS/ROWS mappings: column block fastest, then the other
+// non-axis coordinates, then the split.
+__device__ __forceinline__ void decode_unit(const PartialsPlan& pp, long long u, long long col,
+                                            long long* ib, long long* pb, long long* split) {
+  const ReduceDims& rd = pp.dims;
+  long long rest = u / pp.col_blocks;
+  long long other = rest % pp.others;
+  *split = rest / pp.others;
+  long long in_base = rd.in_offset;
+  long long p_base = rd.out_offset + *split * rd.out_axis_stride;
+#pragma unroll
+  for (int k = 0; k < kMaxDims; ++k) {
+    if (k >= rd.n) break;
+    long long c;
+    if (k == pp.col_dim) {
+      c = col;
+    } else {
+      c = other % rd.ext[k];
+      other /= rd.ext[k];
+    }
+    in_base += c * rd.is[k];
+    p_base += c * rd.os[k];
+  }
+  *ib = in_base;
+  *pb = p_base;
+}
+
+// COLUMNS: wavefront lane t holds column cb*64 + t and all 32 plane lanes of its
+// cube: plane lane l folds rows start + l + 32k in k order; the register tree is
+// the plane's xor tree.
+template <typename Fold, typename T>
+__device__ __forceinline__ void partials_columns(void* partials_ptr, const void* in_ptr,
+                                                 const PartialsPlan& pp, long long chunk_len,
+                                                 long long splits, Fold f) {
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const ReduceDims& rd = pp.dims;
+  const long long stride = rd.axis_stride;
+  const int t = threadIdx.x % kWave;
+  const long long nwaves = static_cast<long long>(gridDim.x) * blockDim.x / kWave;
+  for (long long u = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+       u < pp.units; u += nwaves) {
+    const long long col = (u % pp.col_blocks) * kWave + t;
+    if (col >= pp.columns) continue;
+    long long ib, pb, split;
+    decode_unit(pp, u, col, &ib, &pb, &split);
+    const long long start = split * chunk_len;
+    const long long end = split + 1 == splits ? rd.axis_len : start + chunk_len;
+    const T* x = in + ib;
+    T acc[kWarp];
+#pragma unroll
+    for (int l = 0; l < kWarp; ++l) acc[l] = f.seed(x[(start + l) * stride]);
+    long long r0 = start + kWarp;
+    for (; r0 + kWarp <= end; r0 += kWarp) {
+      T v[kWarp];
+#pragma unroll
+      for (int l = 0; l < kWarp; ++l) v[l] = x[(r0 + l) * stride];
+#pragma unroll
+      for (int l = 0; l < kWarp; ++l) acc[l] = f.fold(acc[l], v[l]);
+    }
+#pragma unroll
+    for (int l = 0; l < kWarp; ++l) {
+      if (r0 + l < end) acc[l] = f.fold(acc[l], x[(r0 + l) * stride]);
+    }
+    partials[pb] = register_tree<kWarp>(acc, f);
+  }
+}
+
+// ROWS: C = 64 / P columns; wavefront lane t = ro*C + c holds column c and the
+// plane lanes ro + P*a (a < A = 32 / P) of its cube, so one load reads P
+// consecutive rows of all C columns. Xor offsets below P cross lanes (a
+// wavefront exchange at lane distance off*C), the rest combine registers.
+template <int A, typename Fold, typename T>
+__device__ __forceinline__ void partials_rows(void* partials_ptr, const void* in_ptr,
+                                              const PartialsPlan& pp, long long chunk_len,
+                                              long long splits, Fold f) {
+  constexpr int P = kWarp / A;
+  constexpr int C = kWave / P;
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const ReduceDims& rd = pp.dims;
+  const long long stride = rd.axis_stride;
+  const int t = threadIdx.x % kWave;
+  const int c = t % C;
+  const int ro = t / C;
+  const long long nwaves = static_cast<long long>(gridDim.x) * blockDim.x / kWave;
+  for (long long u = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+       u < pp.units; u += nwaves) {
+    long long ib, pb, split;
+    decode_unit(pp, u, c, &ib, &pb, &split);
+    const long long start = split * chunk_len;
+    const long long len = (split + 1 == splits ? rd.axis_len : start + chunk_len) - start;
+    const T* x = in + ib + start * stride;
+    T acc[A];
+#pragma unroll
+    for (int a = 0; a < A; ++a) acc[a] = f.seed(x[(ro + P * a) * stride]);
+    long long q0 = kWarp;
+    for (; q0 + kWarp <= len; q0 += kWarp) {
+      T v[A];
+#pragma unroll
+      for (int a = 0; a < A; ++a) v[a] = x[(q0 + ro + P * a) * stride];
+#pragma unroll
+      for (int a = 0; a < A; ++a) acc[a] = f.fold(acc[a], v[a]);
+    }
+#pragma unroll
+    for (int a = 0; a < A; ++a) {
+      if (q0 + ro + P * a < len) acc[a] = f.fold(acc[a], x[(q0 + ro + P * a) * stride]);
+    }
+#pragma unroll
+    for (int off = 1; off < kWarp; off <<= 1) {
+      if (off < P) {
+#pragma unroll
+        for (int a = 0; a < A; ++a) acc[a] = f.combine(acc[a], shfl_xor(acc[a], off * C, kWave));
+      } else {
+        const int s = off / P;
+#pragma unroll
+        for (int a = 0; a < A; a += 2 * s) acc[a] = f.combine(acc[a], acc[a + s]);
+      }
+    }
+    if (ro == 0) partials[pb] = acc[0];
+  }
+}
+
+template <typename Fold, typename T>
+__device__ __forceinline__ void partials_body(void* partials, const void* in,
+                                              const PartialsPlan& pp, long long output_len,
+                                              long long splits, long long chunk_len, Fold f) {
+  if constexpr (VecLanes<T>::value > 0) {
+    if (pp.mode == kPartialsColumns) {
+      partials_columns<Fold, T>(partials, in, pp, chunk_len, splits, f);
+      return;
+    }
+    if (pp.mode == kPartialsRows) {
+      switch (pp.columns) {
+        case 2: partials_rows<1, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
+        case 4: partials_rows<2, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
+        case 8: partials_rows<4, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
+        case 16: partials_rows<8, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
+        case 32: partials_rows<16, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
+        default: break;
+      }
+    }
+  }
+  partials_planes<Fold, T>(partials, in, pp, output_len, splits, chunk_len, f);
+}
+
+// Fold dispatch for element type T over the reference's supported pairs
+// (reduce.cu:765-852): SUM/PROD numeric, SUM_SQUARES float, MAX/MIN ordered;
+// an unsupported op performs no work.
+template <typename T, typename Fn>
+__device__ __forceinline__ void dispatch_fold(int op, Fn&& fn) {
+  constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
+  constexpr bool kOrdered = kFloat || std::is_same_v<T, int> || std::is_same_v<T, long long>;
+  switch (op) {
+    case T4A_CUDA_REDUCE_SUM: fn(SumFold{}); break;
+    case T4A_CUDA_REDUCE_PROD: fn(ProdFold{}); break;
+    case T4A_CUDA_REDUCE_SUM_SQUARES:
+      if constexpr (kFloat) fn(SumSquaresFold{});
+      break;
+    case T4A_CUDA_REDUCE_MAX:
+      if constexpr (kOrdered) fn(MaxFold{});
+      break;
+    case T4A_CUDA_REDUCE_MIN:
+      if constexpr (kOrdered) fn(MinFold{});
+      break;
+    default: break;
+  }
+}
+
+template <typename Fn>
+__device__ __forceinline__ void dispatch_dtype(int dtype, Fn&& fn) {
+  switch (dtype) {
+    case T4A_CUDA_F32: fn(static_cast<float*>(nullptr)); break;
+    case T4A_CUDA_F64: fn(static_cast<double*>(nullptr)); break;
+    case T4A_CUDA_I32: fn(static_cast<int*>(nullptr)); break;
+    case T4A_CUDA_I64: fn(static_cast<long long*>(nullptr)); break;
+    case T4A_CUDA_C32: fn(static_cast<c32*>(nullptr)); break;
+    case T4A_CUDA_C64: fn(static_cast<c64*>(nullptr)); break;
+    default: break;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void reduce_run(void* out, const void* in, int op, bool plane,
+                                           const ReduceDims& rd, long long output_len,
+                                           unsigned char* warp_lds) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    if (plane) {
+      plane_body<decltype(fold), T>(out, in, rd, output_len, fold, warp_lds);
+    } else {
+      unit_body<decltype(fold), T>(out, in, rd, output_len, fold);
+    }
+  });
+}
+
+// ---- kernels the launchers use: one per element type (and pass-1 mapping), the
+// plan computed on the host and passed by value. ----
+
+template <typename T>
+__global__ void __launch_bounds__(512)
+    reduce_kernel(void* out, const void* in, int op, int strategy, ReduceDims rd,
+                  long long output_len) {
+  __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(T)];
+  reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    partials_plane_kernel(void* partials, const void* in, int op, PartialsPlan pp,
+                          long long output_len, long long splits, long long chunk_len) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len, fold);
+  });
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    partials_sideways_kernel(void* partials, const void* in, int op, PartialsPlan pp,
+                             long long output_len, long long splits, long long chunk_len) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    partials_body<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len, fold);
+  });
+}
+
+}  // namespace
+}  // namespace t4a
+
+// ---- the reference entry symbols -----------------------------------------------------
+// Complete kernels for callers that load the code object and launch by name
+// (reference docs/abi/c-kernel-abi.md:3-7): the plan is derived in the kernel
+// from the entry's own arguments, and pass 1 keeps the plane mapping (any
+// geometry that planes the cubes computes the same partials).
+
+extern "C" __global__ void __launch_bounds__(512)
+    t4a_cuda_reduce(void* out, const void* in, int dtype, int op, int strategy,
+                    t4a_cuda_layout out_layout, t4a_cuda_layout in_layout, int axis,
+                    long long output_len) {
+  __shared__ t4a::ReduceDims rd;
+  __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
+  if (threadIdx.x == 0) t4a::reduce_dims(&rd, out_layout, in_layout, axis);
+  __syncthreads();
+  const bool plane = strategy == T4A_CUDA_REDUCE_PLANE;
+  t4a::dispatch_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds);
+  });
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_reduce_partials(void* partials, const void* in, int dtype, int op,
+                             t4a_cuda_layout partials_layout, t4a_cuda_layout in_layout,
+                             int axis, long long output_len, long long splits,
+                             long long chunk_len) {
+  __shared__ t4a::PartialsPlan pp;
+  if (threadIdx.x == 0) {
+    const int w = blockDim.x <= 32u ? static_cast<int>(blockDim.x) : t4a::kWarp;
+    t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, w, 0);
+  }
+  __syncthreads();
+  t4a::dispatch_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    t4a::dispatch_fold<T>(op, [&](auto fold) {
+      t4a::partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
+                                              fold);
+    });
+  });
+}
+
+// ---- launchers -----------------------------------------------------------------------
+
+namespace {
+
+bool launch_empty(const t4a_launch* l) {
+  return l->grid[0] == 0 || l->grid[1] == 0 || l->grid[2] == 0;
+}
+
+template <typename Fn>
+int with_dtype(int dtype, Fn&& fn) {
+  switch (dtype) {
+    case T4A_CUDA_F32: return fn(static_cast<float*>(nullptr));
+    case T4A_CUDA_F64: return fn(static_cast<double*>(nullptr));
+    case T4A_CUDA_I32: return fn(static_cast<int*>(nullptr));
+    case T4A_CUDA_I64: return fn(static_cast<long long*>(nullptr));
+    case T4A_CUDA_C32: return fn(static_cast<t4a::c32*>(nullptr));
+    case T4A_CUDA_C64: return fn(static_cast<t4a::c64*>(nullptr));
+    default: return T4A_OK;  // unknown tag: no work, as the reference entry
+  }
+}
+
+int status_of_last_launch() {
+  return hipGetLastError() == hipSuccess ? T4A_OK : T4A_HIP_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int strategy,
+                              const t4a_cuda_layout* out_layout,
+                              const t4a_cuda_layout* in_layout, int axis, long long output_len,
+                              const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  t4a::ReduceDims rd;
+  t4a::reduce_dims(&rd, *out_layout, *in_layout, axis);
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    hipLaunchKernelGGL(t4a::reduce_kernel<T>, grid, block, 0, static_cast<hipStream_t>(stream),
+                       out, in, op, strategy, rd, output_len);
+    return status_of_last_launch();
+  });
+}
+
+extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
+                                       const t4a_cuda_layout* partials_layout,
+                                       const t4a_cuda_layout* in_layout, int axis,
+                                       long long output_len, long long splits,
+                                       long long chunk_len, const t4a_launch* launch,
+                                       void* stream) {
+  if (launch == nullptr || partials_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (partials == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const unsigned threads = launch->block[0] * launch->block[1] * launch->block[2];
+  const int w = threads <= 32u ? static_cast<int>(threads) : t4a::kWarp;
+  const bool whole_waves = launch->block[1] == 1 && launch->block[2] == 1 && threads >= 64u &&
+                           threads % 64u == 0;
+  t4a::PartialsPlan pp;
+  t4a::partials_plan(&pp, *partials_layout, *in_layout, axis, output_len, splits, w,
+                     whole_waves && t4a::sideways_dtype(dtype));
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  const bool sideways = pp.mode != t4a::kPartialsPlane;
+  return with_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if (sideways) {
+      hipLaunchKernelGGL(t4a::partials_sideways_kernel<T>, grid, block, 0,
+                         static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
+                         splits, chunk_len);
+    } else {
+      hipLaunchKernelGGL(t4a::partials_plane_kernel<T>, grid, block, 0,
+                         static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
+                         splits, chunk_len);
+    }
+    return status_of_last_launch();
+  });
+}

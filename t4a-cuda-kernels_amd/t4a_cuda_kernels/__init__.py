@@ -1,0 +1,391 @@
+"""Host-side mirror of the reference crate `t4a_cuda_kernels` (reference src/lib.rs)
+for the movement and single-axis reduction path, over the MI355X C ABI.
+
+Names, argument order and error behaviour follow the reference: a planner
+returns a `Launch` (or `ReductionPlan`) or raises `T4aError` carrying the
+reference `Error` variant for the same bad input. Geometry is this library's
+MI355X geometry. Launching lives in `t4a_cuda_kernels.hip` (raw device
+pointers and a HIP stream, the caller owning both).
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from ctypes import byref, c_int, c_longlong
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+from . import _lib
+from ._lib import CLaunch, CLayout, CReductionPlan, CSplit, CTransposeConfig
+
+MAX_RANK = 8
+ABI_REVISION = 14
+FLAT_BLOCK = 256
+PLANE_BLOCK = 32
+PLANE_WIDTHS = (8, 16, 32)
+MIN_CHUNK_PLANES = 8
+MAX_SPLITS = 4096
+MAX_GRID_X = 2**31 - 1
+MAX_GRID_YZ = 65535
+DEFAULT_SHARED_BYTES = 48 * 1024
+
+
+class DType(enum.IntEnum):
+    """Element type tags (reference src/lib.rs:151-215)."""
+
+    F32 = 0
+    F64 = 1
+    I32 = 2
+    I64 = 3
+    Bool = 4
+    C32 = 5
+    C64 = 6
+
+    @property
+    def tag(self) -> int:
+        return int(self)
+
+    @property
+    def size(self) -> int:
+        return {0: 4, 1: 8, 2: 4, 3: 8, 4: 1, 5: 8, 6: 16}[int(self)]
+
+
+class ReduceOp(enum.IntEnum):
+    """Reduction operation tags (reference src/lib.rs:3065-3127)."""
+
+    Sum = 0
+    Prod = 1
+    SumSquares = 2
+    Max = 3
+    Min = 4
+
+    @property
+    def tag(self) -> int:
+        return int(self)
+
+    def combine(self) -> "ReduceOp":
+        """Operation of the combine pass: squared partials combine by a sum."""
+        return ReduceOp.Sum if self is ReduceOp.SumSquares else self
+
+    def supports(self, dtype: DType) -> bool:
+        if self in (ReduceOp.Sum, ReduceOp.Prod):
+            return dtype in (DType.F32, DType.F64, DType.I32, DType.I64, DType.C32, DType.C64)
+        if self is ReduceOp.SumSquares:
+            return dtype in (DType.F32, DType.F64)
+        return dtype in (DType.F32, DType.F64, DType.I32, DType.I64)
+
+
+class ReduceStrategy(enum.IntEnum):
+    Unit = 0
+    Plane = 1
+
+    @property
+    def tag(self) -> int:
+        return int(self)
+
+
+class Error(enum.IntEnum):
+    """The reference `Error` enum (src/lib.rs:217-274); the C status is value + 1."""
+
+    RankOutOfRange = 0
+    RankLength = 1
+    NegativeExtent = 2
+    NegativeCount = 3
+    Overflow = 4
+    CountMismatch = 5
+    OffsetOutOfSpan = 6
+    BroadcastDestination = 7
+    UnsupportedDType = 8
+    NotElementwise = 9
+    LaunchLimit = 10
+    InvalidTransposeConfig = 11
+    InvalidAxis = 12
+    DuplicateAxis = 13
+    NotCompact = 14
+    ShapeMismatch = 15
+    InvalidStep = 16
+    InvalidPadding = 17
+    DomainTooLarge = 18
+    InvalidStride = 19
+    StrategyMismatch = 20
+    InvalidPlaneWidth = 21
+    InvalidSplit = 22
+    IndexVectorMismatch = 23
+    UnsupportedOp = 24
+
+
+class T4aError(Exception):
+    """A planner refusal (`error` is the reference variant) or a launch failure."""
+
+    def __init__(self, status: int):
+        self.status = status
+        self.error: Optional[Error] = Error(status - 1) if 1 <= status <= 25 else None
+        name = _lib.load().t4a_status_name(status).decode()
+        super().__init__(f"{name} (status {status})")
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise T4aError(status)
+
+
+class Layout:
+    """Logical strided layout, axis 0 fastest (reference src/lib.rs:322-450)."""
+
+    __slots__ = ("_c",)
+
+    def __init__(self, extents: Sequence[int], strides: Sequence[int], offset: int = 0):
+        if len(extents) != len(strides):
+            raise T4aError(Error.RankLength + 1)
+        rank = len(extents)
+        c = CLayout()
+        ext = (c_longlong * max(rank, 1))(*extents)
+        st = (c_longlong * max(rank, 1))(*strides)
+        _check(_lib.load().t4a_layout_new(byref(c), rank, ext, st, offset))
+        self._c = c
+
+    @classmethod
+    def compact(cls, extents: Sequence[int]) -> "Layout":
+        strides, stride = [], 1
+        for e in extents:
+            strides.append(stride)
+            stride *= e
+        if len(extents) > MAX_RANK:
+            raise T4aError(Error.RankOutOfRange + 1)
+        if stride >= 2**63:
+            raise T4aError(Error.Overflow + 1)
+        return cls(extents, strides, 0)
+
+    @classmethod
+    def from_c(cls, c: CLayout) -> "Layout":
+        out = cls.__new__(cls)
+        out._c = c
+        return out
+
+    @property
+    def c(self) -> CLayout:
+        return self._c
+
+    @property
+    def rank(self) -> int:
+        return self._c.rank
+
+    @property
+    def offset(self) -> int:
+        return self._c.offset
+
+    @property
+    def extents(self) -> list[int]:
+        return list(self._c.extents[: self.rank])
+
+    @property
+    def strides(self) -> list[int]:
+        return list(self._c.strides[: self.rank])
+
+    def element_count(self) -> int:
+        n = c_longlong()
+        _check(_lib.load().t4a_layout_element_count(byref(self._c), byref(n)))
+        return n.value
+
+    def _reach(self, maximum: bool) -> int:
+        total = self.offset
+        for e, s in zip(self.extents, self.strides):
+            step = (e - 1) * s
+            total += max(step, 0) if maximum else min(step, 0)
+        return total
+
+    def min_reachable_offset(self) -> int:
+        return self._reach(False)
+
+    def max_reachable_offset(self) -> int:
+        return self._reach(True)
+
+    def is_compact(self) -> bool:
+        if self.offset != 0:
+            return False
+        stride = 1
+        for e, s in zip(self.extents, self.strides):
+            if s != stride:
+                return False
+            stride *= e
+        return True
+
+    def __eq__(self, other: object) -> bool:
+        return (isinstance(other, Layout) and self.extents == other.extents
+                and self.strides == other.strides and self.offset == other.offset)
+
+    def __repr__(self) -> str:
+        return f"Layout(extents={self.extents}, strides={self.strides}, offset={self.offset})"
+
+
+@dataclass(frozen=True)
+class TransposeConfig:
+    """Tiled-transpose configuration (reference src/lib.rs:452-517)."""
+
+    tile: int
+    block_rows: int
+    padding: int
+    vector_width: int
+
+    def __post_init__(self):
+        c = CTransposeConfig()
+        _check(_lib.load().t4a_transpose_config_new(
+            self.tile, self.block_rows, self.padding, self.vector_width, byref(c)))
+
+    @property
+    def c(self) -> CTransposeConfig:
+        return CTransposeConfig(self.tile, self.block_rows, self.padding, self.vector_width)
+
+    def shared_bytes(self, element_size: int) -> int:
+        return self.tile * (self.tile + self.padding) * element_size
+
+
+TransposeConfig.DEFAULT = TransposeConfig(16, 8, 1, 1)
+
+
+class RankVariant(enum.IntEnum):
+    Fast = 0
+    General = 1
+
+
+@dataclass(frozen=True)
+class Launch:
+    """Planned geometry (reference src/lib.rs:840-873)."""
+
+    grid: tuple
+    block: tuple
+    shared_bytes: int
+    variant: RankVariant = RankVariant.Fast
+
+    @classmethod
+    def from_c(cls, c: CLaunch) -> "Launch":
+        return cls(tuple(c.grid), tuple(c.block), c.shared_bytes, RankVariant(c.variant))
+
+    def to_c(self) -> CLaunch:
+        c = CLaunch()
+        c.grid[:] = list(self.grid)
+        c.block[:] = list(self.block)
+        c.shared_bytes = self.shared_bytes
+        c.variant = int(self.variant)
+        return c
+
+    def is_empty(self) -> bool:
+        return 0 in self.grid
+
+
+@dataclass(frozen=True)
+class Split:
+    splits: int
+    chunk_len: int
+
+    def to_c(self) -> CSplit:
+        return CSplit(self.splits, self.chunk_len)
+
+
+@dataclass(frozen=True)
+class ReductionPlan:
+    """`Direct` fills strategy/launch; `Split` fills split/pass1/combine_*/pass2."""
+
+    kind: str
+    strategy: Optional[ReduceStrategy] = None
+    launch: Optional[Launch] = None
+    split: Optional[Split] = None
+    pass1: Optional[Launch] = None
+    combine_strategy: Optional[ReduceStrategy] = None
+    combine_op: Optional[ReduceOp] = None
+    pass2: Optional[Launch] = None
+
+
+def _layout(x) -> CLayout:
+    return x.c if isinstance(x, Layout) else x
+
+
+def plan_materialize_strided(dtype: DType, src: Layout, src_len: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_materialize_strided(int(dtype), byref(_layout(src)), src_len,
+                                                    byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_strided_to_strided(dtype: DType, src: Layout, src_len: int, dst: Layout,
+                            dst_len: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_strided_to_strided(int(dtype), byref(_layout(src)), src_len,
+                                                   byref(_layout(dst)), dst_len, byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_tiled_transpose(dtype: DType, config: TransposeConfig, src_offset: int,
+                         batch_stride: int, dst_fast_extent: int, src_fast_extent: int,
+                         batches: int, src_len: int, dst_len: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_tiled_transpose(
+        int(dtype), config.c, src_offset, batch_stride, dst_fast_extent, src_fast_extent,
+        batches, src_len, dst_len, byref(out)))
+    return Launch.from_c(out)
+
+
+def split_policy(reduce_len: int, plane_width: int) -> Optional[Split]:
+    has = c_int()
+    out = CSplit()
+    _check(_lib.load().t4a_split_policy(reduce_len, plane_width, byref(has), byref(out)))
+    return Split(out.splits, out.chunk_len) if has.value else None
+
+
+def plan_reduce(dtype: DType, op: ReduceOp, strategy: ReduceStrategy, out_layout: Layout,
+                out_len: int, in_layout: Layout, in_len: int, axis: int,
+                plane_width: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_reduce(int(dtype), int(op), int(strategy),
+                                       byref(_layout(out_layout)), out_len,
+                                       byref(_layout(in_layout)), in_len, axis, plane_width,
+                                       byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_reduce_partials(dtype: DType, op: ReduceOp, partials_layout: Layout,
+                         partials_len: int, in_layout: Layout, in_len: int, axis: int,
+                         split: Split, plane_width: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_reduce_partials(int(dtype), int(op),
+                                                byref(_layout(partials_layout)), partials_len,
+                                                byref(_layout(in_layout)), in_len, axis,
+                                                split.to_c(), plane_width, byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_reduction(dtype: DType, op: ReduceOp, out_layout: Layout, out_len: int,
+                   in_layout: Layout, in_len: int, axis: int,
+                   plane_width: int) -> ReductionPlan:
+    p = CReductionPlan()
+    _check(_lib.load().t4a_plan_reduction(int(dtype), int(op), byref(_layout(out_layout)),
+                                          out_len, byref(_layout(in_layout)), in_len, axis,
+                                          plane_width, byref(p)))
+    if p.kind == 0:
+        return ReductionPlan("Direct", strategy=ReduceStrategy(p.strategy),
+                             launch=Launch.from_c(p.launch))
+    return ReductionPlan("Split", split=Split(p.split.splits, p.split.chunk_len),
+                         pass1=Launch.from_c(p.pass1),
+                         combine_strategy=ReduceStrategy(p.combine_strategy),
+                         combine_op=ReduceOp(p.combine_op), pass2=Launch.from_c(p.pass2))
+
+
+def reduction_partials_layout(in_layout: Layout, axis: int, splits: int) -> Layout:
+    out = CLayout()
+    _check(_lib.load().t4a_reduction_partials_layout(byref(_layout(in_layout)), axis, splits,
+                                                     byref(out)))
+    return Layout.from_c(out)
+
+
+def abi_revision() -> int:
+    return _lib.load().t4a_abi_revision()
+
+
+__all__ = [
+    "ABI_REVISION", "DEFAULT_SHARED_BYTES", "DType", "Error", "FLAT_BLOCK", "Launch", "Layout",
+    "MAX_GRID_X", "MAX_GRID_YZ", "MAX_RANK", "MAX_SPLITS", "MIN_CHUNK_PLANES", "PLANE_BLOCK",
+    "PLANE_WIDTHS", "RankVariant", "ReduceOp", "ReduceStrategy", "ReductionPlan", "Split",
+    "T4aError", "TransposeConfig", "abi_revision", "plan_materialize_strided",
+    "plan_reduce", "plan_reduce_partials", "plan_reduction", "plan_strided_to_strided",
+    "plan_tiled_transpose", "reduction_partials_layout", "split_policy",
+]

@@ -1,0 +1,98 @@
+"""Launch the gfx950 kernels through the C ABI (include/t4a/t4a.h, t4a_hip_*).
+
+Pointers are device addresses (ints, or objects with `data_ptr()` such as torch
+tensors); `stream` is a HIP stream handle (int), an object with `cuda_stream`
+(a torch stream), or None for the null stream. The caller owns every buffer,
+the stream and completion, as with the reference entries
+(reference docs/abi/c-kernel-abi.md:3-14). Nothing here synchronizes.
+"""
+from __future__ import annotations
+
+from ctypes import byref, c_void_p
+from typing import Optional
+
+from . import (DType, Launch, Layout, ReduceOp, ReduceStrategy, ReductionPlan,
+               T4aError, TransposeConfig, _lib, reduction_partials_layout)
+
+
+def _ptr(x) -> c_void_p:
+    if hasattr(x, "data_ptr"):
+        return c_void_p(x.data_ptr())
+    return c_void_p(int(x))
+
+
+def _stream(stream) -> c_void_p:
+    if stream is None:
+        return c_void_p(0)
+    if hasattr(stream, "cuda_stream"):
+        return c_void_p(stream.cuda_stream)
+    return c_void_p(int(stream))
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise T4aError(status)
+
+
+def tiled_transpose(dst, src, dtype: DType, src_offset: int, batch_stride: int,
+                    dst_fast_extent: int, src_fast_extent: int, config: TransposeConfig,
+                    launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_tiled_transpose (cuda/src/movement.cu:571-573)."""
+    _check(_lib.load().t4a_hip_tiled_transpose(
+        _ptr(dst), _ptr(src), int(dtype), src_offset, batch_stride, dst_fast_extent,
+        src_fast_extent, config.c, byref(launch.to_c()), _stream(stream)))
+
+
+def materialize_strided(dst, src, dtype: DType, src_layout: Layout, length: int,
+                        launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_materialize_strided (cuda/src/movement.cu:535-537)."""
+    _check(_lib.load().t4a_hip_materialize_strided(
+        _ptr(dst), _ptr(src), int(dtype), byref(src_layout.c), length, byref(launch.to_c()),
+        _stream(stream)))
+
+
+def strided_to_strided(dst, src, dtype: DType, src_layout: Layout, dst_layout: Layout,
+                       length: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_strided_to_strided (cuda/src/movement.cu:553-556)."""
+    _check(_lib.load().t4a_hip_strided_to_strided(
+        _ptr(dst), _ptr(src), int(dtype), byref(src_layout.c), byref(dst_layout.c), length,
+        byref(launch.to_c()), _stream(stream)))
+
+
+def reduce(out, inp, dtype: DType, op: ReduceOp, strategy: ReduceStrategy,
+           out_layout: Layout, in_layout: Layout, axis: int, output_len: int, launch: Launch,
+           stream=None) -> None:
+    """Reference t4a_cuda_reduce (cuda/src/reduce.cu:765-768)."""
+    _check(_lib.load().t4a_hip_reduce(
+        _ptr(out), _ptr(inp), int(dtype), int(op), int(strategy), byref(out_layout.c),
+        byref(in_layout.c), axis, output_len, byref(launch.to_c()), _stream(stream)))
+
+
+def reduce_partials(partials, inp, dtype: DType, op: ReduceOp, partials_layout: Layout,
+                    in_layout: Layout, axis: int, output_len: int, splits: int,
+                    chunk_len: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_reduce_partials (cuda/src/reduce.cu:813-817)."""
+    _check(_lib.load().t4a_hip_reduce_partials(
+        _ptr(partials), _ptr(inp), int(dtype), int(op), byref(partials_layout.c),
+        byref(in_layout.c), axis, output_len, splits, chunk_len, byref(launch.to_c()),
+        _stream(stream)))
+
+
+def enqueue_reduction(plan: ReductionPlan, out, inp, partials, dtype: DType, op: ReduceOp,
+                      out_layout: Layout, in_layout: Layout, axis: int, output_len: int,
+                      stream=None) -> Optional[Layout]:
+    """Enqueue a planned reduction: the direct pass, or pass 1 then the combine
+    pass on the same stream with no host wait between them (the reference
+    caller's sequence, tests/gpu_reduce_golden.rs:416-441). `partials` must hold
+    the element count of `reduction_partials_layout(in_layout, axis, splits)`.
+    Returns the partials layout of a split plan."""
+    if plan.kind == "Direct":
+        reduce(out, inp, dtype, op, plan.strategy, out_layout, in_layout, axis, output_len,
+               plan.launch, stream)
+        return None
+    partials_layout = reduction_partials_layout(in_layout, axis, plan.split.splits)
+    reduce_partials(partials, inp, dtype, op, partials_layout, in_layout, axis, output_len,
+                    plan.split.splits, plan.split.chunk_len, plan.pass1, stream)
+    reduce(out, partials, dtype, plan.combine_op, plan.combine_strategy, out_layout,
+           partials_layout, axis, output_len, plan.pass2, stream)
+    return partials_layout
