@@ -1,0 +1,331 @@
+"""Benchmark: effective GB/s and HBM-roofline fraction of the movement and
+single-axis reduction path on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]` prints ONE
+JSON line. The default workload is BASELINE.json's configs[1] (C2): f32
+[8192, 8192] sum and max over the inner (contiguous) and the outer axis, and an
+i64 sum over the inner axis, each a planned reduction (pass 1 + combine)
+launched through the C ABI. One step = those five reductions over one input
+set. Inputs are resident in HBM before timing; three input sets rotate so a
+step never finds its input in the 256 MB Infinity Cache left by the previous
+step.
+
+Effective bytes = logical input bytes read once + logical output bytes written
+once (partials excluded), 1 GB = 1e9 B. `roofline` is the dominant kernel's
+algorithmic bytes per launch over its average launch time, measured here with
+HIP events on the launch stream, against the 8 TB/s HBM peak. `cpu_baseline` is
+the CPU oracle (the reference algorithm restated in C, one thread) on a bounded
+sample of the same workload.
+
+Other workloads (--workload c1|c1big|c3|c4|c5) run the other BASELINE configs
+the same way; they are for development, the driver's line is c2.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Callable
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "t4a-cuda-kernels_amd"))
+sys.path.insert(0, str(REPO))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+import t4a_cuda_kernels as t  # noqa: E402
+from t4a_cuda_kernels import hip  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+ROTATE = 3
+
+
+@dataclass
+class Op:
+    """One planned entry (or planned reduction) over rotating buffer sets."""
+
+    name: str
+    kernel: str                      # dominant kernel's name, for the roofline
+    algo_bytes: int                  # logical input + output bytes
+    launch: Callable[[int], None]    # enqueue the op on buffer set r
+    dominant: Callable[[int], None]  # enqueue only the dominant kernel
+    dominant_bytes: int              # algorithmic bytes of the dominant kernel
+    cpu: Callable[[], float] | None = None  # CPU oracle on a sample; returns bytes
+
+
+@dataclass
+class Workload:
+    name: str
+    description: str
+    dtype: str
+    ops: list[Op] = field(default_factory=list)
+
+
+def _stream():
+    return torch.cuda.current_stream()
+
+
+def _rand_f32(n, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.rand(n, generator=g, device="cuda", dtype=torch.float32) * 2 - 1
+
+
+def reduction_op(name, dtype, op, in_ext, axis, sets, cpu_sample=None) -> Op:
+    """A planned reduction over compact `in_ext` (reference axis order)."""
+    in_l = t.Layout.compact(in_ext)
+    oe = list(in_ext)
+    oe[axis] = 1
+    out_l = t.Layout.compact(oe)
+    n, on = in_l.element_count(), out_l.element_count()
+    plan = t.plan_reduction(dtype, op, out_l, on, in_l, n, axis, 32)
+    es = dtype.size
+    out = torch.empty(on * es, dtype=torch.uint8, device="cuda")
+    if plan.kind == "Split":
+        pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
+        part = torch.empty(pl.element_count() * es, dtype=torch.uint8, device="cuda")
+    else:
+        pl, part = None, None
+
+    def launch(r):
+        hip.enqueue_reduction(plan, out, sets[r], part, dtype, op, out_l, in_l, axis, on,
+                              _stream())
+
+    def dominant(r):
+        if plan.kind == "Split":
+            hip.reduce_partials(part, sets[r], dtype, op, pl, in_l, axis, on,
+                                plan.split.splits, plan.split.chunk_len, plan.pass1, _stream())
+        else:
+            hip.reduce(out, sets[r], dtype, op, plan.strategy, out_l, in_l, axis, on,
+                       plan.launch, _stream())
+
+    kernel = "reduce_partials" if plan.kind == "Split" else "reduce"
+    return Op(name, kernel, (n + on) * es, launch, dominant, (n + (pl.element_count() if pl else on)) * es,
+              cpu_sample)
+
+
+def transpose_op(name, dtype, m, n, sets, outs) -> Op:
+    plan = t.plan_tiled_transpose(dtype, t.TransposeConfig.DEFAULT, 0, m * n, m, n, 1, m * n,
+                                  m * n)
+    cfg = t.TransposeConfig.DEFAULT
+
+    def launch(r):
+        hip.tiled_transpose(outs[r], sets[r], dtype, 0, m * n, m, n, cfg, plan, _stream())
+
+    return Op(name, "tiled_transpose", 2 * m * n * dtype.size, launch, launch,
+              2 * m * n * dtype.size)
+
+
+def move_op(name, dtype, src_l, dst_l, sets, outs) -> Op:
+    count = src_l.element_count()
+    src_len = src_l.max_reachable_offset() + 1
+    dst_len = dst_l.max_reachable_offset() + 1
+    plan = t.plan_strided_to_strided(dtype, src_l, src_len, dst_l, dst_len)
+
+    def launch(r):
+        hip.strided_to_strided(outs[r], sets[r], dtype, src_l, dst_l, count, plan, _stream())
+
+    return Op(name, "strided_to_strided", 2 * count * dtype.size, launch, launch,
+              2 * count * dtype.size)
+
+
+# ---- workloads ---------------------------------------------------------------------
+
+def cpu_c2_sample():
+    """Oracle: f32 sum over the inner axis of a 1024-row slice of C2, plus the
+    same slice's outer-axis sum (one thread)."""
+    from oracle import t4a_oracle as orc
+
+    rng = np.random.default_rng(1)
+    rows = 1024
+    x = rng.uniform(-1, 1, 8192 * rows).astype(np.float32)
+    moved = 0
+    for axis, ext in ((0, [8192, rows]), (1, [8192, rows])):
+        in_l = t.Layout.compact(ext)
+        oe = list(ext)
+        oe[axis] = 1
+        out_l = t.Layout.compact(oe)
+        on = out_l.element_count()
+        plan = t.plan_reduction(t.DType.F32, t.ReduceOp.Sum, out_l, on, in_l, x.size, axis, 32)
+        pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
+        part = np.zeros(pl.element_count(), dtype=np.float32)
+        out = np.zeros(on, dtype=np.float32)
+        orc.reduce_partials(part, x, t.DType.F32, t.ReduceOp.Sum, 32, pl, in_l, axis, on,
+                            plan.split.splits, plan.split.chunk_len)
+        orc.reduce(out, part, t.DType.F32, t.ReduceOp.Sum, plan.combine_strategy, 32, out_l, pl,
+                   axis, on)
+        moved += (x.size + on) * 4
+    return moved
+
+
+def build_c2() -> Workload:
+    w = Workload("c2", "C2: f32 [8192,8192] sum+max over inner and outer axis, i64 [8192,8192] "
+                 "sum over the inner axis (planned split reductions)", "f32,i64")
+    ext = [8192, 8192]  # C-shape [8192, 8192]: reference axis 0 is the inner one
+    f = [_rand_f32(8192 * 8192, 10 + r) for r in range(ROTATE)]
+    g = torch.Generator(device="cuda").manual_seed(99)
+    i64 = [torch.randint(-1000, 1001, (8192 * 8192,), generator=g, device="cuda",
+                         dtype=torch.int64) for _ in range(ROTATE)]
+    w.ops.append(reduction_op("sum_f32_inner", t.DType.F32, t.ReduceOp.Sum, ext, 0, f,
+                              cpu_c2_sample))
+    w.ops.append(reduction_op("max_f32_inner", t.DType.F32, t.ReduceOp.Max, ext, 0, f))
+    w.ops.append(reduction_op("sum_f32_outer", t.DType.F32, t.ReduceOp.Sum, ext, 1, f))
+    w.ops.append(reduction_op("max_f32_outer", t.DType.F32, t.ReduceOp.Max, ext, 1, f))
+    w.ops.append(reduction_op("sum_i64_inner", t.DType.I64, t.ReduceOp.Sum, ext, 0, i64))
+    return w
+
+
+def build_c1(m: int) -> Workload:
+    w = Workload(f"c1-{m}", f"C1: tiled transpose f32 [{m},{m}] (1,0)", "f32")
+    sets = [_rand_f32(m * m, r) for r in range(ROTATE)]
+    outs = [torch.empty_like(s) for s in sets]
+    w.ops.append(transpose_op(f"transpose_f32_{m}", t.DType.F32, m, m, sets, outs))
+    return w
+
+
+def build_c3() -> Workload:
+    w = Workload("c3", "C3: strided_to_strided C-[64,128,64,32] perm (3,1,0,2), reversed "
+                 "axis, f64 and c32", "f64,c32")
+    src_l = t.Layout([64, 64, 128, 32], [32, 262144, -2048, 1], 260096)
+    dst_l = t.Layout.compact([64, 64, 128, 32])
+    for dt in (t.DType.F64, t.DType.C32):
+        sets = [torch.empty(16777216 * dt.size, dtype=torch.uint8, device="cuda").random_()
+                for _ in range(ROTATE)]
+        outs = [torch.empty_like(s) for s in sets]
+        w.ops.append(move_op(f"permute4_{dt.name}", dt, src_l, dst_l, sets, outs))
+    return w
+
+
+def build_c4() -> Workload:
+    w = Workload("c4", "C4: f32 C-[32,1048576,4] sumsq+min over the middle axis, i32 prod "
+                 "over the last axis", "f32,i32")
+    ext = [4, 1048576, 32]
+    f = [torch.randn(4 * 1048576 * 32, device="cuda") for _ in range(ROTATE)]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    vals = torch.tensor([-1, 1, 2], dtype=torch.int32, device="cuda")
+    i32 = [vals[torch.randint(0, 3, (4 * 1048576 * 32,), generator=g, device="cuda")]
+           for _ in range(ROTATE)]
+    w.ops.append(reduction_op("sumsq_f32_middle", t.DType.F32, t.ReduceOp.SumSquares, ext, 1, f))
+    w.ops.append(reduction_op("min_f32_middle", t.DType.F32, t.ReduceOp.Min, ext, 1, f))
+    w.ops.append(reduction_op("prod_i32_last", t.DType.I32, t.ReduceOp.Prod, ext, 0, i32))
+    return w
+
+
+def build_c5() -> Workload:
+    w = Workload("c5", "C5: c64 [16]^6 permute (5,2,0,4,1,3) then sum over C-axis 3", "c64")
+    src_l = t.Layout([16] * 6, [256, 65536, 16, 1048576, 4096, 1], 0)
+    dst_l = t.Layout.compact([16] * 6)
+    sets = [torch.empty(16 ** 6 * 16, dtype=torch.uint8, device="cuda").random_()
+            for _ in range(ROTATE)]
+    outs = [torch.empty_like(s) for s in sets]
+    w.ops.append(move_op("permute6_c64", t.DType.C64, src_l, dst_l, sets, outs))
+    # the sum reads the permuted (compact) tensor
+    w.ops.append(reduction_op("sum_c64_axis3", t.DType.C64, t.ReduceOp.Sum, [16] * 6, 2, outs))
+    return w
+
+
+WORKLOADS = {
+    "c2": build_c2,
+    "c1": lambda: build_c1(1024),
+    "c1big": lambda: build_c1(8192),
+    "c3": build_c3,
+    "c4": build_c4,
+    "c5": build_c5,
+}
+
+
+def time_ops(fn: Callable[[int], None], count: int) -> float:
+    """Average milliseconds per call of `fn` over `count` calls, events on the
+    launch stream."""
+    s = _stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(s)
+    for i in range(count):
+        fn(i % ROTATE)
+    stop.record(s)
+    stop.synchronize()
+    return start.elapsed_time(stop) / count
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
+              f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    w = WORKLOADS[args.workload]()
+    step = lambda r: [op.launch(r) for op in w.ops]  # noqa: E731
+    for i in range(args.warmup):
+        step(i % ROTATE)
+    torch.cuda.synchronize()
+    ms_per_step = time_ops(step, args.steps)
+    step_bytes = sum(op.algo_bytes for op in w.ops)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Per-op and dominant-kernel timings (same stream, same rotation).
+    breakdown = {}
+    dom = None
+    for op in w.ops:
+        op_ms = time_ops(op.launch, max(args.steps, 10))
+        k_ms = time_ops(op.dominant, max(args.steps, 10))
+        breakdown[op.name] = {
+            "ms": round(op_ms, 5), "GBps": round(op.algo_bytes / (op_ms * 1e-3) / 1e9, 1),
+            "kernel": op.kernel, "kernel_ms": round(k_ms, 5),
+            "kernel_GBps": round(op.dominant_bytes / (k_ms * 1e-3) / 1e9, 1)}
+        if dom is None or k_ms > dom[1]:
+            dom = (op, k_ms)
+    op, k_ms = dom
+    achieved = op.dominant_bytes / (k_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": f"{op.kernel} ({op.name})", "kernel_ms": round(k_ms, 5)}
+
+    cpu = None
+    cpu_ops = [o for o in w.ops if o.cpu is not None]
+    if cpu_ops and not args.no_cpu:
+        t0 = time.perf_counter()
+        moved = cpu_ops[0].cpu()
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(moved / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "CPU oracle (reference topology restated in C, 1 thread): f32 sum "
+                         "over the inner and the outer axis of a [1024, 8192] slice of C2, "
+                         "pass 1 + combine", "seconds": round(dt, 3)}
+
+    print(json.dumps({
+        "metric": "effective GB/s + % HBM roofline: transpose, strided permute, axis reduce",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (uniform/normal/integer inputs of the config's shape, seeded)",
+        "config": {"workload": w.description, "global_batch": 1, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "breakdown": breakdown,
+    }))
+
+
+if __name__ == "__main__":
+    main()

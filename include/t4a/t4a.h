@@ -186,6 +186,10 @@ int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
                             long long splits, long long chunk_len, const t4a_launch* launch,
                             void* stream);
 
+/* The hipError_t of the most recent launch on this thread that returned
+ * T4A_HIP_ERR_LAUNCH (0 if none). */
+int t4a_hip_last_error(void);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

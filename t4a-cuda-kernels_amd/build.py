@@ -16,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent
@@ -64,13 +65,17 @@ def build(verbose: bool = False) -> Path:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
     ]
+    hip_cmds = []
     for src in HIP_SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
-        cmd = [hipcc, *hip_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd))
-        _run(cmd)
+        hip_cmds.append([hipcc, *hip_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)])
         objects.append(obj)
+    # The translation units are independent: compile them side by side.
+    with ThreadPoolExecutor(max_workers=len(hip_cmds)) as pool:
+        for cmd in hip_cmds:
+            if verbose:
+                print(" ".join(cmd))
+        list(pool.map(_run, hip_cmds))
     OUT_DIR.mkdir(exist_ok=True)
     out = OUT_DIR / LIB_NAME
     tmp = out.with_suffix(".so.tmp")

@@ -386,14 +386,27 @@ extern "C" __global__ void __launch_bounds__(256)
 // ---- launchers -----------------------------------------------------------------------
 
 namespace {
+thread_local int last_launch_error = 0;
+}  // namespace
+
+namespace t4a {
+int status_of_last_launch() {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return T4A_OK;
+  last_launch_error = static_cast<int>(e);
+  return T4A_HIP_ERR_LAUNCH;
+}
+}  // namespace t4a
+
+extern "C" int t4a_hip_last_error(void) { return last_launch_error; }
+
+namespace {
+using t4a::status_of_last_launch;
 
 bool launch_empty(const t4a_launch* l) {
   return l->grid[0] == 0 || l->grid[1] == 0 || l->grid[2] == 0;
 }
 
-int status_of_last_launch() {
-  return hipGetLastError() == hipSuccess ? T4A_OK : T4A_HIP_ERR_LAUNCH;
-}
 
 template <typename Fn>
 int with_payload(int dtype, Fn&& fn) {

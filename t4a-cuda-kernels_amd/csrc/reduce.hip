@@ -27,6 +27,9 @@
 #include "t4a/t4a.h"
 
 namespace t4a {
+// Launch status of the last kernel launch on this thread (movement.hip).
+int status_of_last_launch();
+
 namespace {
 
 template <typename T>
@@ -606,9 +609,7 @@ int with_dtype(int dtype, Fn&& fn) {
   }
 }
 
-int status_of_last_launch() {
-  return hipGetLastError() == hipSuccess ? T4A_OK : T4A_HIP_ERR_LAUNCH;
-}
+using t4a::status_of_last_launch;
 
 }  // namespace
 

@@ -120,8 +120,14 @@ class T4aError(Exception):
     def __init__(self, status: int):
         self.status = status
         self.error: Optional[Error] = Error(status - 1) if 1 <= status <= 25 else None
-        name = _lib.load().t4a_status_name(status).decode()
-        super().__init__(f"{name} (status {status})")
+        lib = _lib.load()
+        name = lib.t4a_status_name(status).decode()
+        detail = ""
+        if status == 100:  # T4A_HIP_ERR_LAUNCH: name the runtime's error
+            code = lib.t4a_hip_last_error()
+            from . import hipmem
+            detail = f": {hipmem.hip().hipGetErrorString(code).decode()} (hipError {code})"
+        super().__init__(f"{name} (status {status}){detail}")
 
 
 def _check(status: int) -> None:

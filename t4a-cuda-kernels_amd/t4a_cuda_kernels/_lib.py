@@ -97,6 +97,7 @@ SIGNATURES = {
                                    POINTER(CReductionPlan)]),
     "t4a_reduction_partials_layout": (c_int, [POINTER(CLayout), c_uint, c_longlong,
                                               POINTER(CLayout)]),
+    "t4a_hip_last_error": (c_int, []),
     "t4a_hip_tiled_transpose": (c_int, [c_void_p, c_void_p, c_int, c_longlong, c_longlong,
                                         c_longlong, c_longlong, CTransposeConfig,
                                         POINTER(CLaunch), c_void_p]),

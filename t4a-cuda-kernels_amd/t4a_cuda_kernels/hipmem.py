@@ -1,0 +1,178 @@
+"""Device buffers, streams and events over the HIP runtime libt4a_hip.so links.
+
+The C ABI leaves device memory and streams to the caller. This module is the
+Python caller's side of that: a thin ctypes layer over the same
+`libamdhip64.so.7` the kernels' library is linked against, so pointers, streams
+and launches all live in one runtime. (torch ships a separate HIP runtime of
+its own; mixing its streams or allocations with this library's launches in one
+process is not supported, so the tests and the benchmark use this module.)
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import byref, c_float, c_int, c_size_t, c_void_p
+
+import numpy as np
+
+from . import _lib
+
+H2D, D2H, D2D = 1, 2, 3
+_HIP = None
+
+
+def hip() -> ctypes.CDLL:
+    """The HIP runtime already mapped by libt4a_hip.so (same soname, same handle)."""
+    global _HIP
+    if _HIP is None:
+        _lib.load()
+        lib = ctypes.CDLL("libamdhip64.so.7")
+        lib.hipMalloc.argtypes = [ctypes.POINTER(c_void_p), c_size_t]
+        lib.hipFree.argtypes = [c_void_p]
+        lib.hipMemcpy.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        lib.hipMemcpyAsync.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_void_p]
+        lib.hipMemset.argtypes = [c_void_p, c_int, c_size_t]
+        lib.hipGetErrorString.restype = ctypes.c_char_p
+        lib.hipGetErrorString.argtypes = [c_int]
+        lib.hipGetDeviceCount.argtypes = [ctypes.POINTER(c_int)]
+        lib.hipStreamCreate.argtypes = [ctypes.POINTER(c_void_p)]
+        lib.hipStreamDestroy.argtypes = [c_void_p]
+        lib.hipStreamSynchronize.argtypes = [c_void_p]
+        lib.hipEventCreate.argtypes = [ctypes.POINTER(c_void_p)]
+        lib.hipEventDestroy.argtypes = [c_void_p]
+        lib.hipEventRecord.argtypes = [c_void_p, c_void_p]
+        lib.hipEventSynchronize.argtypes = [c_void_p]
+        lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(c_float), c_void_p, c_void_p]
+        lib.hipDeviceGetName.argtypes = [ctypes.c_char_p, c_int, c_int]
+        _HIP = lib
+    return _HIP
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = hip().hipGetErrorString(status).decode()
+        raise HipError(f"{what}: {msg} ({status})")
+
+
+def device_count() -> int:
+    n = c_int(0)
+    status = hip().hipGetDeviceCount(byref(n))
+    return n.value if status == 0 else 0
+
+
+def device_name(device: int = 0) -> str:
+    buf = ctypes.create_string_buffer(256)
+    check(hip().hipDeviceGetName(buf, 256, device), "hipDeviceGetName")
+    return buf.value.decode()
+
+
+def synchronize() -> None:
+    check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class DeviceBuffer:
+    """`nbytes` of device memory, freed with the object."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = c_void_p()
+        check(hip().hipMalloc(byref(p), max(self.nbytes, 1)), f"hipMalloc({self.nbytes})")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, extra: int = 0, fill: int | None = None):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes + extra)
+        if fill is not None:
+            buf.fill(fill)
+        buf.upload(arr)
+        return buf
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        if arr.nbytes:
+            check(hip().hipMemcpy(c_void_p(self.ptr + offset), c_void_p(arr.ctypes.data),
+                                  arr.nbytes, H2D), "hipMemcpy H2D")
+
+    def download(self, nbytes: int | None = None) -> np.ndarray:
+        n = self.nbytes if nbytes is None else int(nbytes)
+        out = np.empty(n, dtype=np.uint8)
+        if n:
+            check(hip().hipMemcpy(c_void_p(out.ctypes.data), c_void_p(self.ptr), n, D2H),
+                  "hipMemcpy D2H")
+        return out
+
+    def copy_from(self, other: "DeviceBuffer") -> None:
+        n = min(self.nbytes, other.nbytes)
+        check(hip().hipMemcpy(c_void_p(self.ptr), c_void_p(other.ptr), n, D2D), "hipMemcpy D2D")
+
+    def fill(self, byte: int) -> None:
+        check(hip().hipMemset(c_void_p(self.ptr), int(byte), self.nbytes), "hipMemset")
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None):
+            hip().hipFree(c_void_p(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A HIP stream of default priority."""
+
+    def __init__(self):
+        s = c_void_p()
+        check(hip().hipStreamCreate(byref(s)), "hipStreamCreate")
+        self.handle = s.value
+
+    @property
+    def cuda_stream(self) -> int:
+        return self.handle or 0
+
+    def synchronize(self) -> None:
+        check(hip().hipStreamSynchronize(c_void_p(self.handle)), "hipStreamSynchronize")
+
+    def __del__(self):
+        try:
+            if self.handle:
+                hip().hipStreamDestroy(c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        e = c_void_p()
+        check(hip().hipEventCreate(byref(e)), "hipEventCreate")
+        self.handle = e.value
+
+    def record(self, stream: Stream | None = None) -> None:
+        s = c_void_p(stream.handle if stream is not None else 0)
+        check(hip().hipEventRecord(c_void_p(self.handle), s), "hipEventRecord")
+
+    def synchronize(self) -> None:
+        check(hip().hipEventSynchronize(c_void_p(self.handle)), "hipEventSynchronize")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = c_float()
+        check(hip().hipEventElapsedTime(byref(ms), c_void_p(self.handle), c_void_p(end.handle)),
+              "hipEventElapsedTime")
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                hip().hipEventDestroy(c_void_p(self.handle))
+        except Exception:
+            pass

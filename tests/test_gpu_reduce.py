@@ -1,0 +1,276 @@
+"""Single-axis reductions on the GPU against the CPU oracle.
+
+The kernels keep the reference's fold topology, so for NaN-free inputs every
+partial and every final must equal the oracle's bit for bit -- floats included.
+Where a NaN comes out of an add or multiply only its NaN-ness is compared (the
+payload is the hardware's; reference docs/abi/c-kernel-abi.md:364-366); max/min
+select an operand and stay bit-exact. Independently of the topology, float
+finals are also checked against the reference tests' f64 sequential sum within
+the stated tolerance: relative 1e-5 (f32/c32) or 1e-12 (f64/c64) scaled by
+sqrt(n) (reference tests/gpu_reduce.rs:40-130).
+
+Covered: unit and plane direct passes at plane widths 8/16/32, the wide combine
+widths 64..512, split reductions over contiguous axes (grouped walk, aligned and
+not), strided axes in all three pass-1 mappings (planes, 64+ columns, 2..32
+columns), complex and integer types, non-compact outputs, and the configuration
+shapes C2, C4 and C5.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import t4a_cuda_kernels as t
+from t4a_cuda_kernels import hip
+from gpu_util import NUMPY, say, sentinel, stream, to_device, to_host
+from oracle import t4a_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+Sum, Prod, SumSq, Max, Min = (t.ReduceOp.Sum, t.ReduceOp.Prod, t.ReduceOp.SumSquares,
+                              t.ReduceOp.Max, t.ReduceOp.Min)
+F32, F64, I32, I64, C32, C64 = (t.DType.F32, t.DType.F64, t.DType.I32, t.DType.I64,
+                                t.DType.C32, t.DType.C64)
+
+PAIRS = [(d, op) for op in t.ReduceOp for d in (F32, F64, I32, I64, C32, C64) if op.supports(d)]
+
+
+def values(dtype, op, count, rng):
+    """Finite inputs; products stay near one so they neither overflow nor vanish."""
+    if dtype in (I32, I64):
+        if op == Prod:
+            return rng.choice(np.array([-1, 1, 1, 2, 3], dtype=NUMPY[dtype]), count)
+        return rng.integers(-1000, 1001, count).astype(NUMPY[dtype])
+    if op == Prod:
+        re = 1.0 + rng.uniform(-1, 1, count) / 256.0
+        im = rng.uniform(-1, 1, count) / 256.0
+    else:
+        re = rng.uniform(-1.0, 1.0, count)
+        im = rng.uniform(-1.0, 1.0, count)
+    if dtype in (C32, C64):
+        return (re + 1j * im).astype(NUMPY[dtype])
+    return re.astype(NUMPY[dtype])
+
+
+def _nan_equal(dtype, a: np.ndarray, b: np.ndarray) -> bool:
+    """Element bytes equal, or both NaN in every NaN component."""
+    if dtype in (I32, I64):
+        return np.array_equal(a, b)
+    comp = np.float32 if dtype in (F32, C32) else np.float64
+    x = np.ascontiguousarray(a).view(comp)
+    y = np.ascontiguousarray(b).view(comp)
+    xi = x.view(np.uint32 if comp == np.float32 else np.uint64)
+    yi = y.view(np.uint32 if comp == np.float32 else np.uint64)
+    return bool(((xi == yi) | (np.isnan(x) & np.isnan(y))).all())
+
+
+def check_f64_reference(dtype, op, data, in_l, axis, out_l, finals):
+    """Tolerance check of the finals against the sequential f64 reference."""
+    if dtype in (I32, I64) or op in (Max, Min):
+        return
+    on = out_l.element_count()
+    cplx = dtype in (C32, C64)
+    ref = orc.reduce_f64(data, dtype, op, in_l, axis, on, cplx)
+    # finals are in output-layout order; gather them in logical output order
+    got = []
+    for o in range(on):
+        rest, off = o, out_l.offset
+        for e, s in zip(out_l.extents, out_l.strides):
+            off += (rest % e) * s
+            rest //= e
+        got.append(finals[off])
+    got = np.array(got)
+    if cplx:
+        got = np.stack([got.real, got.imag], axis=1).reshape(-1)
+    n = in_l.extents[axis]
+    tol = (1e-5 if dtype in (F32, C32) else 1e-12) * math.sqrt(n)
+    scale = np.maximum(np.abs(ref), 1.0)
+    if op == Sum:  # cancellation: scale by the sum of magnitudes
+        absref = orc.reduce_f64(np.abs(data) if not cplx else
+                                (np.abs(data.real) + 1j * np.abs(data.imag)).astype(data.dtype),
+                                dtype, op, in_l, axis, on, cplx)
+        scale = np.maximum(absref, 1.0)
+    err = np.abs(got.astype(np.float64) - ref)
+    assert (err <= tol * scale).all(), f"max rel err {(err / scale).max()} > {tol}"
+
+
+def run(dtype, op, in_l, axis, out_l, width, data, *, plan=None, explicit=None):
+    """Plan (or take `explicit` = (strategy, block width) for a direct pass),
+    run the passes on the GPU and in the oracle, compare."""
+    in_len = max(in_l.max_reachable_offset() + 1, 1)
+    out_len = max(out_l.max_reachable_offset() + 1, 1)
+    on = out_l.element_count()
+    es = dtype.size
+    say("reduce", dtype.name, op.name, in_l, "axis", axis, "->", out_l, "w", width, explicit)
+    if explicit is None:
+        plan = plan or t.plan_reduction(dtype, op, out_l, out_len, in_l, in_len, axis, width)
+    else:
+        strategy, bw = explicit
+        plan = t.ReductionPlan("Direct", strategy=strategy,
+                               launch=t.plan_reduce(dtype, op, strategy, out_l, out_len, in_l,
+                                                    in_len, axis, bw))
+    d_in = to_device(data)
+    d_out = sentinel(out_len * es)
+    want_out = np.frombuffer(bytes([0xCD]) * (out_len * es), dtype=NUMPY[dtype]).copy()
+    if plan.kind == "Direct":
+        hip.reduce(d_out, d_in, dtype, op, plan.strategy, out_l, in_l, axis, on, plan.launch,
+                   stream())
+        bw = plan.launch.block[0] if plan.strategy == t.ReduceStrategy.Plane else width
+        orc.reduce(want_out, data, dtype, op, plan.strategy, bw, out_l, in_l, axis, on)
+    else:
+        pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
+        pn = pl.element_count()
+        d_part = sentinel(pn * es)
+        hip.enqueue_reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, axis, on,
+                              stream())
+        want_part = np.zeros(pn, dtype=NUMPY[dtype])
+        orc.reduce_partials(want_part, data, dtype, op, width, pl, in_l, axis, on,
+                            plan.split.splits, plan.split.chunk_len)
+        got_part = to_host(d_part, pn * es, "partials")
+        assert _nan_equal(dtype, got_part, want_part.view(np.uint8)), "pass-1 partials differ"
+        bw = plan.pass2.block[0] if plan.combine_strategy == t.ReduceStrategy.Plane else width
+        orc.reduce(want_out, want_part, dtype, plan.combine_op, plan.combine_strategy, bw,
+                   out_l, pl, axis, on)
+    got = to_host(d_out, out_len * es, "output")
+    assert _nan_equal(dtype, got, want_out.view(np.uint8)), "finals differ"
+    return plan, got.view(NUMPY[dtype])
+
+
+def compact_case(dtype, op, c_shape, c_axis, width, rng, *, explicit=None):
+    """A C-order shape reduced over C-axis `c_axis` (reference axis r-1-c_axis)."""
+    ext = list(reversed(c_shape))
+    axis = len(c_shape) - 1 - c_axis
+    in_l = t.Layout.compact(ext)
+    oe = list(ext)
+    oe[axis] = 1
+    out_l = t.Layout.compact(oe)
+    data = values(dtype, op, in_l.element_count(), rng)
+    plan, finals = run(dtype, op, in_l, axis, out_l, width, data, explicit=explicit)
+    check_f64_reference(dtype, op, data, in_l, axis, out_l, finals)
+    return plan
+
+
+@pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
+def test_direct_unit_and_plane(dtype, op):
+    rng = np.random.default_rng(100 + 10 * int(dtype) + int(op))
+    for width in (8, 16, 32):
+        for c_shape, c_axis in [((37, 5), 1), ((5, 37), 0), ((3, 7, 11), 1), ((1, 1), 0),
+                                ((300, width), 1), ((width + 3, 9), 0), ((2, 255, 3), 1)]:
+            compact_case(dtype, op, c_shape, c_axis, width, rng)
+
+
+@pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
+def test_wide_plane_widths(dtype, op):
+    rng = np.random.default_rng(200 + 10 * int(dtype) + int(op))
+    for bw in (64, 128, 256, 512):
+        compact_case(dtype, op, (3, bw * 5 + 7), 1, 32, rng,
+                     explicit=(t.ReduceStrategy.Plane, bw))
+        compact_case(dtype, op, (bw + 1, 2), 0, 32, rng, explicit=(t.ReduceStrategy.Plane, bw))
+
+
+@pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
+def test_split_contiguous_axis(dtype, op):
+    rng = np.random.default_rng(300 + 10 * int(dtype) + int(op))
+    for width in (8, 16, 32):
+        for n in (8 * width * 2, 8195, 65541, 100_003):
+            plan = compact_case(dtype, op, (n,), 0, width, rng)
+            assert plan.kind == "Split"
+    compact_case(dtype, op, (3, 20_001), 1, 32, rng)
+
+
+@pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
+def test_split_strided_axis(dtype, op):
+    """Outer axes: 2..32 columns (ROWS), 64+ columns incl. a ragged block
+    (COLUMNS), 3 columns and complex types (plane mapping)."""
+    rng = np.random.default_rng(400 + 10 * int(dtype) + int(op))
+    for cols in (2, 3, 4, 8, 16, 32, 64, 100, 256):
+        compact_case(dtype, op, (2, 1031, cols), 1, 32, rng)
+    compact_case(dtype, op, (700, 5), 0, 16, rng)
+    compact_case(dtype, op, (600, 70), 0, 8, rng)
+
+
+def test_split_unaligned_and_non_compact_output():
+    rng = np.random.default_rng(5)
+    # input at an odd element offset: the grouped walk loads element by element
+    ext = [20_000, 3]
+    in_l = t.Layout(ext, [1, 20_000], 1)
+    out_l = t.Layout([1, 3], [0, 5], 2)  # gaps between outputs
+    for dtype, op in [(F32, Sum), (F64, SumSq), (I32, Max), (I64, Sum)]:
+        data = values(dtype, op, 60_001, rng)
+        run(dtype, op, in_l, 0, out_l, 32, data)
+    # reversed reduce axis (negative stride): serial walk
+    in_l = t.Layout([9000, 4], [-1, 9000], 8999)
+    for dtype, op in [(F32, Sum), (C64, Prod), (I64, Min)]:
+        data = values(dtype, op, 36_000, rng)
+        run(dtype, op, in_l, 0, t.Layout.compact([1, 4]), 32, data)
+
+
+def test_special_values():
+    """NaN wins max/min (bit-exact payloads); an arithmetic NaN stays NaN; signed
+    zeros and infinities."""
+    rng = np.random.default_rng(6)
+    n = 50_000
+    for dtype in (F32, F64):
+        for op in (Sum, Prod, SumSq, Max, Min):
+            data = values(dtype, op, 3 * n, rng)
+            data[5] = np.nan
+            data[n + 17] = np.inf
+            data[n + 4000] = -np.inf
+            data[2 * n:] = -0.0
+            data[2 * n + 77] = 0.0
+            ext = [n, 3]
+            run(dtype, op, t.Layout.compact(ext), 0, t.Layout.compact([1, 3]), 32, data)
+
+
+def test_empty_output_is_no_launch():
+    in_l = t.Layout.compact([5, 0])
+    out_l = t.Layout.compact([1, 0])
+    plan = t.plan_reduction(F32, Sum, out_l, 1, in_l, 1, 0, 32)
+    assert plan.kind == "Direct" and plan.launch.is_empty()
+    d = sentinel(4)
+    hip.reduce(d, d, F32, Sum, plan.strategy, out_l, in_l, 0, 0, plan.launch, stream())
+    to_host(d, 0)
+
+
+# ---- configuration shapes -----------------------------------------------------------
+
+def test_config_c2_f32_inner_and_outer_sum_max_and_i64_sum():
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32)
+    in_l = t.Layout.compact([8192, 8192])
+    for axis, out_ext in ((0, [1, 8192]), (1, [8192, 1])):
+        for op in (Sum, Max):
+            plan, finals = run(F32, op, in_l, axis, t.Layout.compact(out_ext), 32, x)
+            assert plan.kind == "Split" and plan.split.splits == 32
+            check_f64_reference(F32, op, x, in_l, axis, t.Layout.compact(out_ext), finals)
+    xi = rng.integers(-1000, 1001, 8192 * 8192).astype(np.int64)
+    run(I64, Sum, in_l, 0, t.Layout.compact([1, 8192]), 32, xi)
+
+
+def test_config_c4_middle_axis_and_i32_product():
+    rng = np.random.default_rng(3)
+    ext = [4, 1048576, 32]  # C-shape [32, 1048576, 4]
+    in_l = t.Layout.compact(ext)
+    x = rng.standard_normal(in_l.element_count()).astype(np.float32)
+    for op in (SumSq, Min):
+        plan, finals = run(F32, op, in_l, 1, t.Layout.compact([4, 1, 32]), 32, x)
+        assert plan.split.splits == 4096
+        check_f64_reference(F32, op, x, in_l, 1, t.Layout.compact([4, 1, 32]), finals)
+    xi = rng.choice(np.array([-1, 1, 2], dtype=np.int32), in_l.element_count())
+    plan, _ = run(I32, Prod, in_l, 0, t.Layout.compact([1, 1048576, 32]), 32, xi)
+    assert plan.kind == "Direct" and plan.strategy == t.ReduceStrategy.Unit
+
+
+def test_config_c5_sum_over_permuted_axis():
+    """Sum over C-axis 3 of the (5,2,0,4,1,3)-permuted c64 [16]^6 tensor (stored
+    compact after the permute): reference axis 2, stride 256, length 16."""
+    rng = np.random.default_rng(4)
+    ext = [16] * 6
+    in_l = t.Layout.compact(ext)
+    x = (rng.standard_normal(16**6) + 1j * rng.standard_normal(16**6)).astype(np.complex128)
+    out_ext = list(ext)
+    out_ext[2] = 1
+    out_l = t.Layout.compact(out_ext)
+    plan, finals = run(C64, Sum, in_l, 2, out_l, 32, x)
+    assert plan.kind == "Direct" and plan.strategy == t.ReduceStrategy.Unit
+    check_f64_reference(C64, Sum, x, in_l, 2, out_l, finals)
