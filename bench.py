@@ -36,10 +36,9 @@ sys.path.insert(0, str(REPO / "t4a-cuda-kernels_amd"))
 sys.path.insert(0, str(REPO))
 
 import numpy as np  # noqa: E402
-import torch  # noqa: E402
 
 import t4a_cuda_kernels as t  # noqa: E402
-from t4a_cuda_kernels import hip  # noqa: E402
+from t4a_cuda_kernels import hip, hipmem  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 ROTATE = 3
@@ -66,13 +65,29 @@ class Workload:
     ops: list[Op] = field(default_factory=list)
 
 
-def _stream():
-    return torch.cuda.current_stream()
+_STREAM = None
 
 
-def _rand_f32(n, seed):
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    return torch.rand(n, generator=g, device="cuda", dtype=torch.float32) * 2 - 1
+def _stream() -> hipmem.Stream:
+    global _STREAM
+    if _STREAM is None:
+        _STREAM = hipmem.Stream()
+    return _STREAM
+
+
+def _sets(host: np.ndarray) -> list:
+    """ROTATE device copies of one host array (distinct addresses, same data)."""
+    first = hipmem.DeviceBuffer.from_array(host)
+    out = [first]
+    for _ in range(ROTATE - 1):
+        b = hipmem.DeviceBuffer(first.nbytes)
+        b.copy_from(first)
+        out.append(b)
+    return out
+
+
+def _empty_like(bufs) -> list:
+    return [hipmem.DeviceBuffer(b.nbytes) for b in bufs]
 
 
 def reduction_op(name, dtype, op, in_ext, axis, sets, cpu_sample=None) -> Op:
@@ -84,10 +99,10 @@ def reduction_op(name, dtype, op, in_ext, axis, sets, cpu_sample=None) -> Op:
     n, on = in_l.element_count(), out_l.element_count()
     plan = t.plan_reduction(dtype, op, out_l, on, in_l, n, axis, 32)
     es = dtype.size
-    out = torch.empty(on * es, dtype=torch.uint8, device="cuda")
+    out = hipmem.DeviceBuffer(on * es)
     if plan.kind == "Split":
         pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
-        part = torch.empty(pl.element_count() * es, dtype=torch.uint8, device="cuda")
+        part = hipmem.DeviceBuffer(pl.element_count() * es)
     else:
         pl, part = None, None
 
@@ -166,10 +181,9 @@ def build_c2() -> Workload:
     w = Workload("c2", "C2: f32 [8192,8192] sum+max over inner and outer axis, i64 [8192,8192] "
                  "sum over the inner axis (planned split reductions)", "f32,i64")
     ext = [8192, 8192]  # C-shape [8192, 8192]: reference axis 0 is the inner one
-    f = [_rand_f32(8192 * 8192, 10 + r) for r in range(ROTATE)]
-    g = torch.Generator(device="cuda").manual_seed(99)
-    i64 = [torch.randint(-1000, 1001, (8192 * 8192,), generator=g, device="cuda",
-                         dtype=torch.int64) for _ in range(ROTATE)]
+    rng = np.random.default_rng(1)
+    f = _sets(rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32))
+    i64 = _sets(rng.integers(-1000, 1001, 8192 * 8192, dtype=np.int64))
     w.ops.append(reduction_op("sum_f32_inner", t.DType.F32, t.ReduceOp.Sum, ext, 0, f,
                               cpu_c2_sample))
     w.ops.append(reduction_op("max_f32_inner", t.DType.F32, t.ReduceOp.Max, ext, 0, f))
@@ -181,8 +195,8 @@ def build_c2() -> Workload:
 
 def build_c1(m: int) -> Workload:
     w = Workload(f"c1-{m}", f"C1: tiled transpose f32 [{m},{m}] (1,0)", "f32")
-    sets = [_rand_f32(m * m, r) for r in range(ROTATE)]
-    outs = [torch.empty_like(s) for s in sets]
+    sets = _sets(np.random.default_rng(0).uniform(-1.0, 1.0, m * m).astype(np.float32))
+    outs = _empty_like(sets)
     w.ops.append(transpose_op(f"transpose_f32_{m}", t.DType.F32, m, m, sets, outs))
     return w
 
@@ -192,10 +206,10 @@ def build_c3() -> Workload:
                  "axis, f64 and c32", "f64,c32")
     src_l = t.Layout([64, 64, 128, 32], [32, 262144, -2048, 1], 260096)
     dst_l = t.Layout.compact([64, 64, 128, 32])
+    rng = np.random.default_rng(2)
     for dt in (t.DType.F64, t.DType.C32):
-        sets = [torch.empty(16777216 * dt.size, dtype=torch.uint8, device="cuda").random_()
-                for _ in range(ROTATE)]
-        outs = [torch.empty_like(s) for s in sets]
+        sets = _sets(rng.standard_normal(16777216 * dt.size // 8))
+        outs = _empty_like(sets)
         w.ops.append(move_op(f"permute4_{dt.name}", dt, src_l, dst_l, sets, outs))
     return w
 
@@ -204,11 +218,9 @@ def build_c4() -> Workload:
     w = Workload("c4", "C4: f32 C-[32,1048576,4] sumsq+min over the middle axis, i32 prod "
                  "over the last axis", "f32,i32")
     ext = [4, 1048576, 32]
-    f = [torch.randn(4 * 1048576 * 32, device="cuda") for _ in range(ROTATE)]
-    g = torch.Generator(device="cuda").manual_seed(3)
-    vals = torch.tensor([-1, 1, 2], dtype=torch.int32, device="cuda")
-    i32 = [vals[torch.randint(0, 3, (4 * 1048576 * 32,), generator=g, device="cuda")]
-           for _ in range(ROTATE)]
+    rng = np.random.default_rng(3)
+    f = _sets(rng.standard_normal(4 * 1048576 * 32).astype(np.float32))
+    i32 = _sets(rng.choice(np.array([-1, 1, 2], dtype=np.int32), 4 * 1048576 * 32))
     w.ops.append(reduction_op("sumsq_f32_middle", t.DType.F32, t.ReduceOp.SumSquares, ext, 1, f))
     w.ops.append(reduction_op("min_f32_middle", t.DType.F32, t.ReduceOp.Min, ext, 1, f))
     w.ops.append(reduction_op("prod_i32_last", t.DType.I32, t.ReduceOp.Prod, ext, 0, i32))
@@ -219,9 +231,8 @@ def build_c5() -> Workload:
     w = Workload("c5", "C5: c64 [16]^6 permute (5,2,0,4,1,3) then sum over C-axis 3", "c64")
     src_l = t.Layout([16] * 6, [256, 65536, 16, 1048576, 4096, 1], 0)
     dst_l = t.Layout.compact([16] * 6)
-    sets = [torch.empty(16 ** 6 * 16, dtype=torch.uint8, device="cuda").random_()
-            for _ in range(ROTATE)]
-    outs = [torch.empty_like(s) for s in sets]
+    sets = _sets(np.random.default_rng(4).standard_normal(16 ** 6 * 2))
+    outs = _empty_like(sets)
     w.ops.append(move_op("permute6_c64", t.DType.C64, src_l, dst_l, sets, outs))
     # the sum reads the permuted (compact) tensor
     w.ops.append(reduction_op("sum_c64_axis3", t.DType.C64, t.ReduceOp.Sum, [16] * 6, 2, outs))
@@ -242,15 +253,14 @@ def time_ops(fn: Callable[[int], None], count: int) -> float:
     """Average milliseconds per call of `fn` over `count` calls, events on the
     launch stream."""
     s = _stream()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    start, stop = hipmem.Event(), hipmem.Event()
+    s.synchronize()
     start.record(s)
     for i in range(count):
         fn(i % ROTATE)
     stop.record(s)
     stop.synchronize()
-    return start.elapsed_time(stop) / count
+    return start.elapsed_ms(stop) / count
 
 
 def main() -> None:
@@ -265,7 +275,7 @@ def main() -> None:
         print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
               f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
-    if not torch.cuda.is_available():
+    if hipmem.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
 
@@ -273,7 +283,7 @@ def main() -> None:
     step = lambda r: [op.launch(r) for op in w.ops]  # noqa: E731
     for i in range(args.warmup):
         step(i % ROTATE)
-    torch.cuda.synchronize()
+    _stream().synchronize()
     ms_per_step = time_ops(step, args.steps)
     step_bytes = sum(op.algo_bytes for op in w.ops)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
