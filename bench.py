@@ -239,7 +239,23 @@ def build_c5() -> Workload:
     return w
 
 
+def build_copy() -> Workload:
+    """The copy ceiling: copy_exact of 256 MiB (f32 [8192, 8192])."""
+    w = Workload("copy", "copy_exact f32 [8192,8192] (the measured copy ceiling)", "f32")
+    n = 8192 * 8192
+    sets = _sets(np.random.default_rng(5).uniform(-1, 1, n).astype(np.float32))
+    outs = _empty_like(sets)
+    plan = t.plan_copy_exact(t.DType.F32, n)
+
+    def launch(r):
+        hip.copy_exact(outs[r], sets[r], t.DType.F32, n, plan, _stream())
+
+    w.ops.append(Op("copy_f32_256MiB", "copy_exact", 2 * n * 4, launch, launch, 2 * n * 4))
+    return w
+
+
 WORKLOADS = {
+    "copy": build_copy,
     "c2": build_c2,
     "c1": lambda: build_c1(1024),
     "c1big": lambda: build_c1(8192),

@@ -116,7 +116,10 @@ int t4a_layout_compact(t4a_cuda_layout* out, int rank, const long long* extents)
 /* Checked extent product (reference Layout::element_count). */
 int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count);
 
-/* ---- movement planners (reference src/lib.rs:1628-1737) ---------------------- */
+/* ---- movement planners (reference src/lib.rs:1592-1737) ---------------------- */
+
+/* Reference plan_copy_exact (src/lib.rs:1624-1626). */
+int t4a_plan_copy_exact(int dtype, long long len, t4a_launch* launch);
 
 int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
                                  t4a_launch* launch);
@@ -166,6 +169,9 @@ int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype, long long src
                             long long batch_stride, long long dst_fast_extent,
                             long long src_fast_extent, t4a_cuda_transpose_config config,
                             const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_copy_exact, cuda/src/movement.cu:528-533. */
+int t4a_hip_copy_exact(void* dst, const void* src, int dtype, long long len,
+                       const t4a_launch* launch, void* stream);
 /* Reference t4a_cuda_materialize_strided, cuda/src/movement.cu:535-537. */
 int t4a_hip_materialize_strided(void* dst, const void* src, int dtype,
                                 const t4a_cuda_layout* src_layout, long long len,

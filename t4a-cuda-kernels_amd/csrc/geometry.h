@@ -368,6 +368,33 @@ T4A_HD void partials_plan(PartialsPlan* p, const t4a_cuda_layout& partials,
   p->units = p->col_blocks * others * splits;
 }
 
+// Whether pass 1 can stream whole runs of cubes through the grouped walk: a
+// regroupable fold over a 4- or 8-byte real or integer type, 32-lane planes, a
+// contiguous axis, every chunk holding at least 32 groups of V = 16 / size
+// elements, and every chunk start a multiple of V elements from the base (the
+// base pointer's own 16-byte alignment is the launcher's to check).
+T4A_HD bool stream_applies(const PartialsPlan& p, int dtype, int op, long long chunk_len,
+                           int plane_width) {
+  if (!sideways_dtype(dtype) || op == T4A_CUDA_REDUCE_PROD) return false;
+  if (op < T4A_CUDA_REDUCE_SUM || op > T4A_CUDA_REDUCE_MIN) return false;
+  if (p.mode != kPartialsPlane || plane_width != kWarp || p.dims.axis_stride != 1) return false;
+  const long long v = 16 / dtype_size(dtype);
+  if (chunk_len / v < kWarp || chunk_len % v != 0 || p.dims.in_offset % v != 0) return false;
+  for (int k = 0; k < p.dims.n; ++k) {
+    if (p.dims.is[k] % v != 0) return false;
+  }
+  return true;
+}
+
+// Cubes each streaming plane takes: enough planes to fill the chip (16384, four
+// wavefronts of two planes on each of 256 CUs, twice over), at most 8 cubes.
+T4A_HD long long stream_cubes_per_plane(long long cubes) {
+  long long per = cubes / 16384;
+  if (per < 1) per = 1;
+  if (per > 8) per = 8;
+  return per;
+}
+
 }  // namespace t4a
 
 #endif  // T4A_GEOMETRY_H_

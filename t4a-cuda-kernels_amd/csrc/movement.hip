@@ -316,8 +316,57 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
   }
 }
 
+// ---- copy_exact -----------------------------------------------------------------------
+// A bit-preserving copy of len elements (reference movement.cu:91-97, entry
+// 528-533). With both pointers 16-byte aligned each thread streams kCopyUnroll
+// 16-byte vectors per iteration (loads first, then stores); the bytes after the
+// last whole vector, and unaligned buffers, go element by element.
+constexpr int kCopyUnroll = 4;
+
+template <typename P>
+__device__ __forceinline__ void copy_elements(void* dst, const void* src, long long first,
+                                              long long len) {
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long i = first + static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < len; i += gstride)
+    d[i] = s[i];
+}
+
+template <typename P>
+__device__ __forceinline__ void copy_body(void* dst, const void* src, long long len) {
+  const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) &
+                        15) == 0;
+  if (!aligned || sizeof(P) > 16) {
+    copy_elements<P>(dst, src, 0, len);
+    return;
+  }
+  const long long vectors = len * static_cast<long long>(sizeof(P)) / 16;
+  Bits128* d = static_cast<Bits128*>(dst);
+  const Bits128* s = static_cast<const Bits128*>(src);
+  const long long tid = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const long long nthreads = static_cast<long long>(gridDim.x) * blockDim.x;
+  long long i = tid;
+  for (; i + (kCopyUnroll - 1) * nthreads < vectors; i += kCopyUnroll * nthreads) {
+    Bits128 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) v[u] = s[i + u * nthreads];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) d[i + u * nthreads] = v[u];
+  }
+  for (; i < vectors; i += nthreads) d[i] = s[i];
+  // Elements after the last whole vector.
+  copy_elements<P>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len);
+}
+
 // ---- kernels the launchers use: one per payload width, the plan computed on
 // the host and passed by value. ----
+
+template <typename P>
+__global__ void __launch_bounds__(256) copy_kernel(void* dst, const void* src, long long len) {
+  copy_body<P>(dst, src, len);
+}
 
 template <typename P>
 __global__ void __launch_bounds__(256)
@@ -366,6 +415,17 @@ extern "C" __global__ void __launch_bounds__(256)
       break;
     default:
       break;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_copy_exact(void* dst, const void* src, int dtype, long long len) {
+  switch (t4a::dtype_size(dtype)) {
+    case 1: t4a::copy_body<uint8_t>(dst, src, len); break;
+    case 4: t4a::copy_body<uint32_t>(dst, src, len); break;
+    case 8: t4a::copy_body<unsigned long long>(dst, src, len); break;
+    case 16: t4a::copy_body<t4a::Elem16>(dst, src, len); break;
+    default: break;
   }
 }
 
@@ -457,6 +517,21 @@ extern "C" int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype,
     hipLaunchKernelGGL(t4a::transpose_kernel<P>, grid, block, 0,
                        static_cast<hipStream_t>(stream), dst, src, src_offset, batch_stride,
                        dst_fast_extent, src_fast_extent);
+    return status_of_last_launch();
+  });
+}
+
+extern "C" int t4a_hip_copy_exact(void* dst, const void* src, int dtype, long long len,
+                                  const t4a_launch* launch, void* stream) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_payload(dtype, [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    hipLaunchKernelGGL(t4a::copy_kernel<P>, grid, block, 0, static_cast<hipStream_t>(stream),
+                       dst, src, len);
     return status_of_last_launch();
   });
 }

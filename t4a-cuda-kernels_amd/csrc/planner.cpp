@@ -285,6 +285,18 @@ int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count) {
   return element_count(layout, count);
 }
 
+// Reference plan_copy_exact -> plan_elementwise (src/lib.rs:1592-1599, 1624-1626): every
+// dtype, flat_launch's refusals; each thread streams four 16-byte vectors.
+int t4a_plan_copy_exact(int dtype, long long len, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (int s = flat_launch_check(len)) return s;
+  long long bytes;
+  if (!checked_mul(len, t4a::dtype_size(dtype), &bytes)) return T4A_ERR_OVERFLOW;
+  set_launch(launch, len == 0 ? 0 : blocks_for(bytes, kBlock * 16 * 4), kBlock, 0);
+  return ok();
+}
+
 // Reference plan_materialize_strided (src/lib.rs:1628-1641).
 int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
                                  t4a_launch* launch) {
@@ -488,8 +500,10 @@ int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_
   t4a::PartialsPlan plan;
   t4a::partials_plan(&plan, *partials_layout, *in_layout, static_cast<int>(axis), output_len,
                      split.splits, t4a::kWarp, t4a::sideways_dtype(dtype));
-  const long long per_block =
+  long long per_block =
       plan.mode == t4a::kPartialsPlane ? kBlock / t4a::kWarp : kBlock / t4a::kWave;
+  if (t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))
+    per_block *= t4a::stream_cubes_per_plane(cubes);  // planes take runs of cubes
   set_launch(launch, plan.units == 0 ? 0 : blocks_for(plan.units, per_block), kBlock, 0);
   return ok();
 }

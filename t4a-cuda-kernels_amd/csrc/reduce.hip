@@ -291,6 +291,108 @@ __device__ __forceinline__ T pass1_walk(const T* __restrict__ in, long long ib, 
   return walk_scalar<Fold, T>(in, ib, stride, start, end, w, lane, f);
 }
 
+// Streaming PLANE mapping for a contiguous axis whose every chunk is 16-byte
+// aligned and holds at least W groups (the host checks both): each 32-lane plane
+// takes a run of consecutive cubes -- consecutive splits of one output, so
+// consecutive memory -- and loads the next cube's first batch of groups before
+// it folds the current one, so two cubes' loads are in flight per lane. Each
+// cube's fold is exactly the grouped walk above; only load issue order changes.
+template <typename Fold, typename T>
+__device__ __forceinline__ void partials_stream(void* partials_ptr, const void* in_ptr,
+                                                const PartialsPlan& pp, long long output_len,
+                                                long long splits, long long chunk_len,
+                                                long long per_plane, Fold f) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int W = kWarp;
+  using G = Group<T, V>;
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const ReduceDims& rd = pp.dims;
+  const int lane = threadIdx.x % W;
+  const long long plane = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / W;
+  const long long cubes = output_len * splits;
+  long long cube = plane * per_plane;
+  const long long stop = cube + per_plane < cubes ? cube + per_plane : cubes;
+  if (cube >= stop) return;
+  // Incremental (output, split) walk: one division per run.
+  long long o = cube / splits;
+  long long split = cube - o * splits;
+  long long ib, pb;
+  decode_output(rd, o, &ib, &pb);
+  const long long last_len = rd.axis_len - (splits - 1) * chunk_len;
+
+  // First batch of a cube: groups lane + kW, k < 4, those below `groups`.
+  auto first_batch = [&](const T* chunk, long long groups, G* b) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k == 0 || lane + k * W < groups)
+        b[k] = reinterpret_cast<const G*>(chunk)[lane + k * W];
+    }
+  };
+  G cur[4];
+  const T* chunk = in + ib + split * chunk_len;
+  long long len = split + 1 == splits ? last_len : chunk_len;
+  first_batch(chunk, len / V, cur);
+  for (;;) {
+    // Next cube's coordinates and first batch.
+    long long n_split = split + 1, n_o = o, n_ib = ib, n_pb = pb;
+    const bool more = cube + 1 < stop;
+    G nxt[4];
+    const T* n_chunk = chunk;
+    long long n_len = 0;
+    if (more) {
+      if (n_split == splits) {
+        n_split = 0;
+        ++n_o;
+        decode_output(rd, n_o, &n_ib, &n_pb);
+      }
+      n_chunk = in + n_ib + n_split * chunk_len;
+      n_len = n_split + 1 == splits ? last_len : chunk_len;
+      first_batch(n_chunk, n_len / V, nxt);
+    }
+    // Fold the current cube (reference reduce.cu:449-525 order).
+    const long long groups = len / V;
+    T acc = group_value<Fold, T, V>(cur[0], f);
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      if (lane + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(cur[k], f));
+    }
+    if (groups > 4 * W) {  // longer chunks: whole batches, then the partial batch
+      long long idx = lane + 4LL * W;
+      G b[4];
+      for (; idx + 3LL * W < groups; idx += 4LL * W) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) b[k] = reinterpret_cast<const G*>(chunk)[idx + k * W];
+        const T lo = f.combine(group_value<Fold, T, V>(b[0], f), group_value<Fold, T, V>(b[1], f));
+        const T hi = f.combine(group_value<Fold, T, V>(b[2], f), group_value<Fold, T, V>(b[3], f));
+        acc = f.combine(acc, f.combine(lo, hi));
+      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        if (idx + k * W < groups) b[k] = reinterpret_cast<const G*>(chunk)[idx + k * W];
+      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        if (idx + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(b[k], f));
+      }
+    }
+    const long long tail = groups * V;
+    if (lane < len - tail) acc = f.fold(acc, chunk[tail + lane]);
+    const T reduced = plane_tree(acc, W, f);
+    if (lane == 0) partials[pb + split * rd.out_axis_stride] = reduced;
+    if (!more) break;
+    ++cube;
+    split = n_split;
+    o = n_o;
+    ib = n_ib;
+    pb = n_pb;
+    chunk = n_chunk;
+    len = n_len;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+  }
+}
+
 // PLANE mapping: plane = W lanes (W = blockDim.x when blockDim.x <= 32, else 32
 // with blockDim.x / 32 planes per block, reference reduce.cu:557-581); planes
 // stride over the cubes.
@@ -537,6 +639,20 @@ __global__ void __launch_bounds__(256)
 
 template <typename T>
 __global__ void __launch_bounds__(256)
+    partials_stream_kernel(void* partials, const void* in, int op, PartialsPlan pp,
+                           long long output_len, long long splits, long long chunk_len,
+                           long long per_plane) {
+  if constexpr (VecLanes<T>::value > 0) {
+    dispatch_fold<T>(op, [&](auto fold) {
+      if constexpr (decltype(fold)::kRegroup)
+        partials_stream<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
+                                           per_plane, fold);
+    });
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
     partials_sideways_kernel(void* partials, const void* in, int op, PartialsPlan pp,
                              long long output_len, long long splits, long long chunk_len) {
   dispatch_fold<T>(op, [&](auto fold) {
@@ -653,9 +769,24 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   const bool sideways = pp.mode != t4a::kPartialsPlane;
+  const bool stream_mode =
+      !sideways && whole_waves &&
+      t4a::stream_applies(pp, dtype, op, chunk_len, w) &&
+      (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  // Streaming planes split the cubes evenly over the launched planes (whole
+  // wavefronts, so at least two planes per block).
+  long long per_plane = 1;
+  if (stream_mode) {
+    const long long planes = static_cast<long long>(grid.x) * (threads / t4a::kWarp);
+    per_plane = (output_len * splits + planes - 1) / planes;
+  }
   return with_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
-    if (sideways) {
+    if (stream_mode) {
+      hipLaunchKernelGGL(t4a::partials_stream_kernel<T>, grid, block, 0,
+                         static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
+                         splits, chunk_len, per_plane);
+    } else if (sideways) {
       hipLaunchKernelGGL(t4a::partials_sideways_kernel<T>, grid, block, 0,
                          static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
                          splits, chunk_len);

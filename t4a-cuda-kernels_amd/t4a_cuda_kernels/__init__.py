@@ -306,6 +306,12 @@ def _layout(x) -> CLayout:
     return x.c if isinstance(x, Layout) else x
 
 
+def plan_copy_exact(dtype: DType, length: int) -> Launch:
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_copy_exact(int(dtype), length, byref(out)))
+    return Launch.from_c(out)
+
+
 def plan_materialize_strided(dtype: DType, src: Layout, src_len: int) -> Launch:
     out = CLaunch()
     _check(_lib.load().t4a_plan_materialize_strided(int(dtype), byref(_layout(src)), src_len,
@@ -391,7 +397,7 @@ __all__ = [
     "ABI_REVISION", "DEFAULT_SHARED_BYTES", "DType", "Error", "FLAT_BLOCK", "Launch", "Layout",
     "MAX_GRID_X", "MAX_GRID_YZ", "MAX_RANK", "MAX_SPLITS", "MIN_CHUNK_PLANES", "PLANE_BLOCK",
     "PLANE_WIDTHS", "RankVariant", "ReduceOp", "ReduceStrategy", "ReductionPlan", "Split",
-    "T4aError", "TransposeConfig", "abi_revision", "plan_materialize_strided",
+    "T4aError", "TransposeConfig", "abi_revision", "plan_copy_exact", "plan_materialize_strided",
     "plan_reduce", "plan_reduce_partials", "plan_reduction", "plan_strided_to_strided",
     "plan_tiled_transpose", "reduction_partials_layout", "split_policy",
 ]

@@ -75,6 +75,7 @@ SIGNATURES = {
                                POINTER(c_longlong), c_longlong]),
     "t4a_layout_compact": (c_int, [POINTER(CLayout), c_int, POINTER(c_longlong)]),
     "t4a_layout_element_count": (c_int, [POINTER(CLayout), POINTER(c_longlong)]),
+    "t4a_plan_copy_exact": (c_int, [c_int, c_longlong, POINTER(CLaunch)]),
     "t4a_plan_materialize_strided": (c_int, [c_int, POINTER(CLayout), c_longlong,
                                              POINTER(CLaunch)]),
     "t4a_plan_strided_to_strided": (c_int, [c_int, POINTER(CLayout), c_longlong,
@@ -101,6 +102,8 @@ SIGNATURES = {
     "t4a_hip_tiled_transpose": (c_int, [c_void_p, c_void_p, c_int, c_longlong, c_longlong,
                                         c_longlong, c_longlong, CTransposeConfig,
                                         POINTER(CLaunch), c_void_p]),
+    "t4a_hip_copy_exact": (c_int, [c_void_p, c_void_p, c_int, c_longlong, POINTER(CLaunch),
+                                   c_void_p]),
     "t4a_hip_materialize_strided": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayout),
                                             c_longlong, POINTER(CLaunch), c_void_p]),
     "t4a_hip_strided_to_strided": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayout),

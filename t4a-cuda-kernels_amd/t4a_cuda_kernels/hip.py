@@ -43,6 +43,12 @@ def tiled_transpose(dst, src, dtype: DType, src_offset: int, batch_stride: int,
         src_fast_extent, config.c, byref(launch.to_c()), _stream(stream)))
 
 
+def copy_exact(dst, src, dtype: DType, length: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_copy_exact (cuda/src/movement.cu:528-533)."""
+    _check(_lib.load().t4a_hip_copy_exact(_ptr(dst), _ptr(src), int(dtype), length,
+                                          byref(launch.to_c()), _stream(stream)))
+
+
 def materialize_strided(dst, src, dtype: DType, src_layout: Layout, length: int,
                         launch: Launch, stream=None) -> None:
     """Reference t4a_cuda_materialize_strided (cuda/src/movement.cu:535-537)."""
