@@ -202,6 +202,69 @@ struct alignas(8) Elem16 {
   unsigned long long lo, hi;
 };
 
+// V payloads moved as one access: a 16-byte vector when V > 1, else the
+// payload at its own alignment (a c64 element is only 8-byte aligned).
+template <typename P, int V>
+struct alignas(V > 1 ? sizeof(P) * V : alignof(P)) Vec {
+  P v[V];
+};
+
+// Streaming (non-temporal) loads and stores of a Vec: data moved once is not
+// kept in the caches. The access width is the Vec's size, split into 8-byte
+// halves when the Vec is only 8-byte aligned.
+using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+using u32x2 = unsigned int __attribute__((ext_vector_type(2)));
+
+template <typename P, int V>
+__device__ __forceinline__ Vec<P, V> nt_load(const P* p) {
+  constexpr int kBytes = static_cast<int>(sizeof(P)) * V;
+  Vec<P, V> out;
+  if constexpr (kBytes == 16 && alignof(Vec<P, V>) == 16) {
+    const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    __builtin_memcpy(&out, &r, 16);
+  } else if constexpr (kBytes == 16) {
+    const u32x2 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    const u32x2 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p) + 1);
+    __builtin_memcpy(&out, &lo, 8);
+    __builtin_memcpy(reinterpret_cast<char*>(&out) + 8, &hi, 8);
+  } else if constexpr (kBytes == 8) {
+    const u32x2 r = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    __builtin_memcpy(&out, &r, 8);
+  } else if constexpr (kBytes == 4) {
+    const unsigned r = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
+    __builtin_memcpy(&out, &r, 4);
+  } else {
+    out = *reinterpret_cast<const Vec<P, V>*>(p);
+  }
+  return out;
+}
+
+template <typename P, int V>
+__device__ __forceinline__ void nt_store(P* p, const Vec<P, V>& x) {
+  constexpr int kBytes = static_cast<int>(sizeof(P)) * V;
+  if constexpr (kBytes == 16 && alignof(Vec<P, V>) == 16) {
+    u32x4 r;
+    __builtin_memcpy(&r, &x, 16);
+    __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+  } else if constexpr (kBytes == 16) {
+    u32x2 lo, hi;
+    __builtin_memcpy(&lo, &x, 8);
+    __builtin_memcpy(&hi, reinterpret_cast<const char*>(&x) + 8, 8);
+    __builtin_nontemporal_store(lo, reinterpret_cast<u32x2*>(p));
+    __builtin_nontemporal_store(hi, reinterpret_cast<u32x2*>(p) + 1);
+  } else if constexpr (kBytes == 8) {
+    u32x2 r;
+    __builtin_memcpy(&r, &x, 8);
+    __builtin_nontemporal_store(r, reinterpret_cast<u32x2*>(p));
+  } else if constexpr (kBytes == 4) {
+    unsigned r;
+    __builtin_memcpy(&r, &x, 4);
+    __builtin_nontemporal_store(r, reinterpret_cast<unsigned*>(p));
+  } else {
+    *reinterpret_cast<Vec<P, V>*>(p) = x;
+  }
+}
+
 }  // namespace t4a
 
 #endif  // T4A_DEVICE_H_

@@ -23,9 +23,10 @@
 
 namespace t4a {
 
-// Threads per block of every MI355X launch this library plans (four 64-lane
-// wavefronts).
+// Threads per block of the MI355X launches this library plans (four 64-lane
+// wavefronts; the tiled transpose runs eight).
 constexpr int kBlock = 256;
+constexpr int kTransposeBlock = 512;
 constexpr int kWave = 64;
 // Lanes of a reference "warp": planes wider than this cross it (reduce.cu:140).
 constexpr int kWarp = 32;
@@ -46,9 +47,9 @@ T4A_HD int dtype_size(int dtype) {
 // ---- tiled transpose ----------------------------------------------------------
 //
 // dst[b*S + i + j*M] = src[src_offset + b*S + i*N + j] (reference
-// docs/abi/c-kernel-abi.md:151-159). A tile is kTileM source rows (i) by
-// kTileN source columns (j), staged through LDS; tile index order is i-tile
-// fastest, then j-tile, then batch, like the reference's (x, y, z) grid.
+// docs/abi/c-kernel-abi.md:151-159). A tile is tile_m source rows (i) by
+// tile_n source columns (j), staged through LDS by one 512-thread block; the
+// batch is the grid's z coordinate, like the reference's (x, y, z) grid.
 struct TransposeTiling {
   int tile_m;
   int tile_n;
@@ -60,10 +61,10 @@ struct TransposeTiling {
 T4A_HD TransposeTiling transpose_tiling(long long m, long long n, long long batches,
                                         int esize) {
   TransposeTiling t;
-  // 64x64 elements for 1-8 byte elements (16-32 KiB of LDS), 32x64 for 16-byte
-  // ones, so one tile row is a 256-1024 byte HBM segment on both sides.
-  t.tile_m = 64;
-  t.tile_n = esize >= 16 ? 32 : 64;
+  // About 64 KiB of LDS per tile: 128 x 128 elements up to 4 bytes, 128 x 64
+  // of 8 bytes, 64 x 64 of 16 bytes.
+  t.tile_m = esize >= 16 ? 64 : 128;
+  t.tile_n = esize >= 8 ? 64 : 128;
   t.tiles_m = (m + t.tile_m - 1) / t.tile_m;
   t.tiles_n = (n + t.tile_n - 1) / t.tile_n;
   t.total = t.tiles_m * t.tiles_n * batches;

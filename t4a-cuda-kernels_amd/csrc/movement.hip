@@ -21,29 +21,34 @@ namespace t4a {
 namespace {
 
 // One LDS arena per block, shared by every payload width's instantiation.
-// Index tables (2 x 64 offsets) plus the largest tile: 64 x 65 payloads of 8
-// bytes, or 64 x 33 of 16 bytes.
+// Movement: index tables (2 x 64 offsets) plus the largest tile, 64 x 65
+// payloads of 8 bytes or 64 x 33 of 16 bytes. Transpose: one tile of
+// TransposeShape below, at most 128 x 65 8-byte payloads.
 constexpr int kMoveLdsBytes = 128 * 8 + 64 * 33 * 16;
-constexpr int kTransposeLdsBytes = 64 * 33 * 16;
-
-// V payloads moved as one access: a 16-byte vector when V > 1, else the
-// payload at its own alignment (a c64 element is only 8-byte aligned).
-template <typename P, int V>
-struct alignas(V > 1 ? sizeof(P) * V : alignof(P)) Vec {
-  P v[V];
-};
+constexpr int kTransposeLdsBytes = 128 * 65 * 8;
 
 // ---- tiled transpose ---------------------------------------------------------------
 
 // dst[b*S + i + j*M] = src[src_offset + b*S + i*N + j] for the batch of
-// blockIdx.z. Tile (i-tile fastest, then j-tile) loops stride over gridDim.x.
-// VL / VS: elements per load / store (a 16-byte vector, or 1).
+// blockIdx.z. A tile is TM source rows (i) by TN source columns (j), about 64
+// KiB of LDS. Tiles are visited in diagonal order -- tile t takes i-tile
+// t % tiles_m and j-tile (t / tiles_m + i-tile) % tiles_n -- so the tiles in
+// flight at once start at different column offsets: with the power-of-two row
+// pitches of typical matrices, i-tile-major order sends every concurrent tile's
+// rows to the same few HBM channels. Both sides stream with non-temporal 16-byte
+// accesses. VL / VS: elements per load / store (a 16-byte vector, or 1).
+template <typename P>
+struct TransposeShape {
+  static constexpr int TM = sizeof(P) >= 16 ? 64 : 128;
+  static constexpr int TN = sizeof(P) >= 8 ? 64 : 128;
+};
+
 template <typename P, int VL, int VS>
 __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __restrict__ src,
                                                 long long src_offset, long long S, long long M,
                                                 long long N, unsigned char* lds) {
-  constexpr int TM = 64;
-  constexpr int TN = sizeof(P) >= 16 ? 32 : 64;
+  constexpr int TM = TransposeShape<P>::TM;
+  constexpr int TN = TransposeShape<P>::TN;
   constexpr int PITCH = TN + 1;
   P* tile = reinterpret_cast<P*>(lds);
   const long long tiles_m = (M + TM - 1) / TM;
@@ -55,8 +60,10 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   for (long long t = blockIdx.x; t < per_batch; t += gridDim.x) {
-    const long long i0 = (t % tiles_m) * TM;
-    const long long j0 = (t / tiles_m) * TN;
+    const long long tm = t % tiles_m;
+    const long long tn = (t / tiles_m + tm) % tiles_n;
+    const long long i0 = tm * TM;
+    const long long j0 = tn * TN;
     const int rows = static_cast<int>(M - i0 < TM ? M - i0 : TM);
     const int cols = static_cast<int>(N - j0 < TN ? N - j0 : TN);
     // Source rows: runs of TN along j. VL divides N and src_offset, so a vector
@@ -65,7 +72,7 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
       const int i = e / (TN / VL);
       const int j = (e % (TN / VL)) * VL;
       if (i < rows && j < cols) {
-        const Vec<P, VL> x = *reinterpret_cast<const Vec<P, VL>*>(s + (i0 + i) * N + j0 + j);
+        const Vec<P, VL> x = nt_load<P, VL>(s + (i0 + i) * N + j0 + j);
 #pragma unroll
         for (int k = 0; k < VL; ++k) tile[i * PITCH + j + k] = x.v[k];
       }
@@ -79,7 +86,7 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
         Vec<P, VS> x;
 #pragma unroll
         for (int k = 0; k < VS; ++k) x.v[k] = tile[(i + k) * PITCH + j];
-        *reinterpret_cast<Vec<P, VS>*>(d + (j0 + j) * M + i0 + i) = x;
+        nt_store<P, VS>(d + (j0 + j) * M + i0 + i, x);
       }
     }
     __syncthreads();
@@ -91,7 +98,7 @@ __device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
                                                    long long src_offset, long long S,
                                                    long long M, long long N,
                                                    unsigned char* lds) {
-  constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
+  constexpr int V = sizeof(P) <= 8 ? 16 / static_cast<int>(sizeof(P)) : 1;
   const bool vl = V > 1 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && N % V == 0 &&
                   src_offset % V == 0;
   const bool vs = V > 1 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 && M % V == 0;
@@ -119,7 +126,62 @@ __device__ __forceinline__ bool transpose_config_valid(const t4a_cuda_transpose_
 // ---- strided movement --------------------------------------------------------------
 
 // TILED: an la x lb tile; element (i, j) sits at src_base + src_a[i] + j and at
-// dst_base + i + dst_b[j]. VL / VS as above.
+// dst_base + i + dst_b[j]. VL / VS: elements per load / store.
+//
+// A block walks tiles t, t + gridDim.x, ... and keeps a tile's loads in flight
+// while it writes the previous one: it loads tile t into registers, parks them
+// in LDS, then issues tile t+1's loads before reading tile t back out of LDS
+// and storing it. Tile coordinates are A-tile fastest, then B-tile, then the
+// batch dims; the second coordinate of extent > 1 is skewed by the first
+// (diagonal order), so tiles in flight together start at different offsets
+// along both runs.
+struct TileCoords {
+  long long sbase, dbase;
+  int va, vb;  // valid run lengths of this tile
+};
+
+__device__ __forceinline__ TileCoords tile_coords(const MovePlan& p, long long t) {
+  const int a_last = p.a_dims[p.na - 1];
+  const int b_last = p.b_dims[p.nb - 1];
+  long long rest = t;
+  long long first = 0;
+  int seen = 0;
+  auto coord = [&](long long extent) {
+    long long c = rest % extent;
+    rest /= extent;
+    if (extent > 1) {
+      if (seen == 1) c = (c + first) % extent;
+      if (seen == 0) first = c;
+      ++seen;
+    }
+    return c;
+  };
+  const long long ta = coord(p.a_tiles);
+  const long long tb = coord(p.b_tiles);
+  TileCoords tc;
+  tc.sbase = p.src_offset + ta * p.a_tile * p.ss[a_last] + tb * p.b_tile * p.ss[b_last];
+  tc.dbase = p.dst_offset + ta * p.a_tile * p.ds[a_last] + tb * p.b_tile * p.ds[b_last];
+  for (int q = 0; q < p.nbatch; ++q) {
+    const int k = p.batch_dims[q];
+    const long long c = coord(p.ext[k]);
+    tc.sbase += c * p.ss[k];
+    tc.dbase += c * p.ds[k];
+  }
+  const long long a_left = p.ext[a_last] - ta * p.a_tile;
+  const long long b_left = p.ext[b_last] - tb * p.b_tile;
+  tc.va = static_cast<int>(p.a_inner * (a_left < p.a_tile ? a_left : p.a_tile));
+  tc.vb = static_cast<int>(p.b_inner * (b_left < p.b_tile ? b_left : p.b_tile));
+  return tc;
+}
+
+// Threads of a pipelined tile block, and the largest tile (elements) of each
+// payload width: the register stage holds a tile's share per thread.
+constexpr int kTileThreads = 256;
+template <typename P>
+constexpr int max_tile_elems() {
+  return sizeof(P) >= 16 ? 64 * 32 : 64 * 64;
+}
+
 template <typename P, int VL, int VS>
 __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restrict__ src,
                                            const MovePlan& p, const long long* src_a,
@@ -128,60 +190,90 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
   const int lb = static_cast<int>(p.lb);
   const int pitch = lb + 1;
   const int tid = threadIdx.x;
-  const int nthreads = blockDim.x;
-  const int a_last = p.a_dims[p.na - 1];
-  const int b_last = p.b_dims[p.nb - 1];
-  for (long long t = blockIdx.x; t < p.tiles; t += gridDim.x) {
-    long long rest = t;
-    const long long ta = rest % p.a_tiles;
-    rest /= p.a_tiles;
-    const long long tb = rest % p.b_tiles;
-    rest /= p.b_tiles;
-    long long sbase = p.src_offset + ta * p.a_tile * p.ss[a_last] + tb * p.b_tile * p.ss[b_last];
-    long long dbase = p.dst_offset + ta * p.a_tile * p.ds[a_last] + tb * p.b_tile * p.ds[b_last];
-    for (int q = 0; q < p.nbatch; ++q) {
-      const int k = p.batch_dims[q];
-      const long long c = rest % p.ext[k];
-      rest /= p.ext[k];
-      sbase += c * p.ss[k];
-      dbase += c * p.ds[k];
-    }
-    const long long a_left = p.ext[a_last] - ta * p.a_tile;
-    const long long b_left = p.ext[b_last] - tb * p.b_tile;
-    const int va = static_cast<int>(p.a_inner * (a_left < p.a_tile ? a_left : p.a_tile));
-    const int vb = static_cast<int>(p.b_inner * (b_left < p.b_tile ? b_left : p.b_tile));
-    const P* s = src + sbase;
-    P* d = dst + dbase;
-    const int lbv = lb / VL;
-    for (int e = tid; e < la * lbv; e += nthreads) {
-      const int i = e / lbv;
-      const int j = (e - i * lbv) * VL;
-      if (i < va && j < vb) {
-        const Vec<P, VL> x = *reinterpret_cast<const Vec<P, VL>*>(s + src_a[i] + j);
-#pragma unroll
-        for (int k = 0; k < VL; ++k) tile[i * pitch + j + k] = x.v[k];
-      }
-    }
-    __syncthreads();
-    const int lav = la / VS;
-    for (int e = tid; e < lb * lav; e += nthreads) {
+  const int lbv = lb / VL;
+  const int lav = la / VS;
+  auto store_tile = [&](const TileCoords& tc) {
+    P* d = dst + tc.dbase;
+    for (int e = tid; e < lb * lav; e += blockDim.x) {
       const int j = e / lav;
       const int i = (e - j * lav) * VS;
-      if (i < va && j < vb) {
+      if (i < tc.va && j < tc.vb) {
         Vec<P, VS> x;
 #pragma unroll
         for (int k = 0; k < VS; ++k) x.v[k] = tile[(i + k) * pitch + j];
-        *reinterpret_cast<Vec<P, VS>*>(d + i + dst_b[j]) = x;
+        nt_store<P, VS>(d + i + dst_b[j], x);
+      }
+    }
+  };
+  long long t = blockIdx.x;
+  if (blockDim.x != kTileThreads) {
+    // Any other block size: load, park, store, one tile at a time.
+    for (; t < p.tiles; t += gridDim.x) {
+      const TileCoords tc = tile_coords(p, t);
+      const P* s = src + tc.sbase;
+      for (int e = tid; e < la * lbv; e += blockDim.x) {
+        const int i = e / lbv;
+        const int j = (e - i * lbv) * VL;
+        if (i < tc.va && j < tc.vb) {
+          const Vec<P, VL> x = nt_load<P, VL>(s + src_a[i] + j);
+#pragma unroll
+          for (int k = 0; k < VL; ++k) tile[i * pitch + j + k] = x.v[k];
+        }
+      }
+      __syncthreads();
+      store_tile(tc);
+      __syncthreads();
+    }
+    return;
+  }
+  constexpr int R = max_tile_elems<P>() / VL / kTileThreads;  // register vectors per thread
+  // This thread's tile slots (row i, column j) are the same for every tile.
+  int slot_i[R], slot_j[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = tid + r * kTileThreads;
+    slot_i[r] = e < la * lbv ? e / lbv : la;  // la: no slot
+    slot_j[r] = e < la * lbv ? (e - slot_i[r] * lbv) * VL : 0;
+  }
+  Vec<P, VL> regs[R];
+  auto load_tile = [&](const TileCoords& tc) {
+    const P* s = src + tc.sbase;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (slot_i[r] < tc.va && slot_j[r] < tc.vb)
+        regs[r] = nt_load<P, VL>(s + src_a[slot_i[r]] + slot_j[r]);
+    }
+  };
+  if (t >= p.tiles) return;
+  TileCoords cur = tile_coords(p, t);
+  load_tile(cur);
+  for (;;) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (slot_i[r] < cur.va && slot_j[r] < cur.vb) {
+#pragma unroll
+        for (int k = 0; k < VL; ++k) tile[slot_i[r] * pitch + slot_j[r] + k] = regs[r].v[k];
       }
     }
     __syncthreads();
+    const long long next = t + gridDim.x;
+    TileCoords nxt = cur;
+    if (next < p.tiles) {
+      nxt = tile_coords(p, next);
+      load_tile(nxt);  // in flight while this tile is stored
+    }
+    store_tile(cur);
+    __syncthreads();
+    if (next >= p.tiles) break;
+    t = next;
+    cur = nxt;
   }
 }
 
 // Offsets of run position `i` along a chain: mixed-radix digits over the
 // chain's extents (the last digit bounded by the tile), times the other side's
 // strides.
-__device__ __forceinline__ long long chain_offset(const MovePlan& p, const int* dims, int count,
+__host__ __device__ inline long long chain_offset(const MovePlan& p, const int* dims, int count,
                                                   long long last_tile, const long long* strides,
                                                   long long i) {
   long long off = 0;
@@ -197,7 +289,7 @@ __device__ __forceinline__ long long chain_offset(const MovePlan& p, const int* 
 // 16-byte accesses along a run need every run start to be a multiple of V:
 // the base offset, every stride outside the run, the tile step of the run's
 // tiled dim, and every partial tile's valid length.
-__device__ __forceinline__ bool run_vectorizable(const MovePlan& p, const int* dims, int count,
+__host__ __device__ inline bool run_vectorizable(const MovePlan& p, const int* dims, int count,
                                                  long long inner, long long tile,
                                                  const long long* strides, long long offset,
                                                  int v, const void* ptr) {
@@ -214,32 +306,53 @@ __device__ __forceinline__ bool run_vectorizable(const MovePlan& p, const int* d
   return true;
 }
 
+// The vector width (elements per 16-byte access) of a payload on the tiled
+// path, and whether the source (VL) and destination (VS) runs take it.
 template <typename P>
-__device__ __forceinline__ void move_tiled(void* dst, const void* src, const MovePlan& p,
-                                           unsigned char* lds) {
+constexpr int tile_vector() {
+  return sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
+}
+
+__host__ __device__ inline void tile_vectorizable(const MovePlan& p, int v, const void* dst,
+                                                  const void* src, bool* vl, bool* vs) {
+  *vl = run_vectorizable(p, p.b_dims, p.nb, p.b_inner, p.b_tile, p.ss, p.src_offset, v, src);
+  *vs = run_vectorizable(p, p.a_dims, p.na, p.a_inner, p.a_tile, p.ds, p.dst_offset, v, dst);
+}
+
+// LDS layout of a tiled block: the two run-offset tables, then the tile.
+__device__ __forceinline__ void tile_tables(const MovePlan& p, unsigned char* lds) {
   long long* src_a = reinterpret_cast<long long*>(lds);
   long long* dst_b = src_a + 64;
-  P* tile = reinterpret_cast<P*>(lds + 128 * sizeof(long long));
   for (int i = threadIdx.x; i < p.la; i += blockDim.x)
     src_a[i] = chain_offset(p, p.a_dims, p.na, p.a_tile, p.ss, i);
   for (int j = threadIdx.x; j < p.lb; j += blockDim.x)
     dst_b[j] = chain_offset(p, p.b_dims, p.nb, p.b_tile, p.ds, j);
   __syncthreads();
-  constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
-  const bool vl = run_vectorizable(p, p.b_dims, p.nb, p.b_inner, p.b_tile, p.ss, p.src_offset,
-                                   V, src);
-  const bool vs = run_vectorizable(p, p.a_dims, p.na, p.a_inner, p.a_tile, p.ds, p.dst_offset,
-                                   V, dst);
-  P* d = static_cast<P*>(dst);
-  const P* s = static_cast<const P*>(src);
+}
+
+template <typename P, int VL, int VS>
+__device__ __forceinline__ void move_tiled_as(void* dst, const void* src, const MovePlan& p,
+                                              unsigned char* lds) {
+  tile_tables(p, lds);
+  const long long* src_a = reinterpret_cast<const long long*>(lds);
+  move_tiles<P, VL, VS>(static_cast<P*>(dst), static_cast<const P*>(src), p, src_a, src_a + 64,
+                        reinterpret_cast<P*>(lds + 128 * sizeof(long long)));
+}
+
+template <typename P>
+__device__ __forceinline__ void move_tiled(void* dst, const void* src, const MovePlan& p,
+                                           unsigned char* lds) {
+  constexpr int V = tile_vector<P>();
+  bool vl, vs;
+  tile_vectorizable(p, V, dst, src, &vl, &vs);
   if (vl && vs) {
-    move_tiles<P, V, V>(d, s, p, src_a, dst_b, tile);
+    move_tiled_as<P, V, V>(dst, src, p, lds);
   } else if (vl) {
-    move_tiles<P, V, 1>(d, s, p, src_a, dst_b, tile);
+    move_tiled_as<P, V, 1>(dst, src, p, lds);
   } else if (vs) {
-    move_tiles<P, 1, V>(d, s, p, src_a, dst_b, tile);
+    move_tiled_as<P, 1, V>(dst, src, p, lds);
   } else {
-    move_tiles<P, 1, 1>(d, s, p, src_a, dst_b, tile);
+    move_tiled_as<P, 1, 1>(dst, src, p, lds);
   }
 }
 
@@ -318,9 +431,9 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
 
 // ---- copy_exact -----------------------------------------------------------------------
 // A bit-preserving copy of len elements (reference movement.cu:91-97, entry
-// 528-533). With both pointers 16-byte aligned each thread streams kCopyUnroll
-// 16-byte vectors per iteration (loads first, then stores); the bytes after the
-// last whole vector, and unaligned buffers, go element by element.
+// 528-533). With both pointers 16-byte aligned the bytes stream as non-temporal
+// 16-byte vectors; the elements after the last whole vector, and unaligned
+// buffers, go element by element.
 constexpr int kCopyUnroll = 4;
 
 template <typename P>
@@ -342,20 +455,25 @@ __device__ __forceinline__ void copy_body(void* dst, const void* src, long long 
     copy_elements<P>(dst, src, 0, len);
     return;
   }
+  // Each block streams one contiguous span of 16-byte vectors, its threads
+  // kCopyUnroll vectors apart per step, loads issued before stores.
+  using V16 = Vec<Bits128, 1>;
   const long long vectors = len * static_cast<long long>(sizeof(P)) / 16;
+  const long long span = (vectors + gridDim.x - 1) / gridDim.x;
+  const long long begin = static_cast<long long>(blockIdx.x) * span;
+  const long long end = begin + span < vectors ? begin + span : vectors;
   Bits128* d = static_cast<Bits128*>(dst);
   const Bits128* s = static_cast<const Bits128*>(src);
-  const long long tid = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const long long nthreads = static_cast<long long>(gridDim.x) * blockDim.x;
-  long long i = tid;
-  for (; i + (kCopyUnroll - 1) * nthreads < vectors; i += kCopyUnroll * nthreads) {
-    Bits128 v[kCopyUnroll];
+  const long long step = blockDim.x;
+  long long i = begin + threadIdx.x;
+  for (; i + (kCopyUnroll - 1) * step < end; i += kCopyUnroll * step) {
+    V16 v[kCopyUnroll];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) v[u] = s[i + u * nthreads];
+    for (int u = 0; u < kCopyUnroll; ++u) v[u] = nt_load<Bits128, 1>(s + i + u * step);
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) d[i + u * nthreads] = v[u];
+    for (int u = 0; u < kCopyUnroll; ++u) nt_store<Bits128, 1>(d + i + u * step, v[u]);
   }
-  for (; i < vectors; i += nthreads) d[i] = s[i];
+  for (; i < end; i += step) nt_store<Bits128, 1>(d + i, nt_load<Bits128, 1>(s + i));
   // Elements after the last whole vector.
   copy_elements<P>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len);
 }
@@ -369,7 +487,7 @@ __global__ void __launch_bounds__(256) copy_kernel(void* dst, const void* src, l
 }
 
 template <typename P>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     transpose_kernel(void* dst, const void* src, long long src_offset, long long batch_stride,
                      long long dst_fast_extent, long long src_fast_extent) {
   __shared__ alignas(16) unsigned char lds[kTransposeLdsBytes];
@@ -377,10 +495,20 @@ __global__ void __launch_bounds__(256)
                         lds);
 }
 
-template <typename P>
-__global__ void __launch_bounds__(256) move_kernel(void* dst, const void* src, MovePlan plan) {
+template <typename P, int VL, int VS>
+__global__ void __launch_bounds__(256)
+    move_tiled_kernel(void* dst, const void* src, MovePlan plan) {
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
-  move_dispatch<P>(dst, src, plan, lds);
+  move_tiled_as<P, VL, VS>(dst, src, plan, lds);
+}
+
+template <typename P>
+__global__ void __launch_bounds__(256) move_flat_kernel(void* dst, const void* src, MovePlan plan) {
+  if (plan.mode == kMoveContig) {
+    move_rows<P>(dst, src, plan);
+  } else {
+    move_elements<P>(dst, src, plan);
+  }
 }
 
 }  // namespace
@@ -388,7 +516,7 @@ __global__ void __launch_bounds__(256) move_kernel(void* dst, const void* src, M
 
 using t4a::kBlock;
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(512)
     t4a_cuda_tiled_transpose(void* dst, const void* src, int dtype, long long src_offset,
                              long long batch_stride, long long dst_fast_extent,
                              long long src_fast_extent, t4a_cuda_transpose_config config) {
@@ -489,10 +617,25 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
                 const t4a_launch* launch, void* stream, int dtype) {
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
-    hipLaunchKernelGGL(t4a::move_kernel<P>, grid, block, 0, static_cast<hipStream_t>(stream),
-                       dst, src, plan);
+    if (plan.mode != t4a::kMoveTiled) {
+      hipLaunchKernelGGL(t4a::move_flat_kernel<P>, grid, block, 0, s, dst, src, plan);
+      return status_of_last_launch();
+    }
+    constexpr int V = t4a::tile_vector<P>();
+    bool vl, vs;
+    t4a::tile_vectorizable(plan, V, dst, src, &vl, &vs);
+    if (vl && vs) {
+      hipLaunchKernelGGL((t4a::move_tiled_kernel<P, V, V>), grid, block, 0, s, dst, src, plan);
+    } else if (vl) {
+      hipLaunchKernelGGL((t4a::move_tiled_kernel<P, V, 1>), grid, block, 0, s, dst, src, plan);
+    } else if (vs) {
+      hipLaunchKernelGGL((t4a::move_tiled_kernel<P, 1, V>), grid, block, 0, s, dst, src, plan);
+    } else {
+      hipLaunchKernelGGL((t4a::move_tiled_kernel<P, 1, 1>), grid, block, 0, s, dst, src, plan);
+    }
     return status_of_last_launch();
   });
 }

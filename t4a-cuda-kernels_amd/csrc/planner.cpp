@@ -138,7 +138,9 @@ int flat_launch_check(long long len) {
 void movement_launch(const t4a::MovePlan& plan, t4a_launch* out) {
   long long blocks = 0;
   switch (plan.mode) {
-    case t4a::kMoveTiled: blocks = blocks_for(plan.tiles, 1); break;
+    // Tiled blocks are persistent: four per CU on 256 CUs, each pipelining its
+    // run of tiles (the next tile's loads overlap the current tile's stores).
+    case t4a::kMoveTiled: blocks = plan.tiles < 1024 ? plan.tiles : 1024; break;
     case t4a::kMoveContig: blocks = blocks_for(plan.len, kBlock * 4); break;
     case t4a::kMoveGeneric: blocks = blocks_for(plan.len, kBlock * 4); break;
     default: blocks = 0; break;
@@ -396,13 +398,13 @@ int t4a_plan_tiled_transpose(int dtype, t4a_cuda_transpose_config config, long l
   if (gx > kMaxGridX || gy > kMaxGridYZ || static_cast<unsigned long long>(batches) > kMaxGridYZ)
     return T4A_ERR_LAUNCH_LIMIT;
   if (gx == 0 || gy == 0 || batches == 0) {
-    set_launch(launch, 0, kBlock, 0);
+    set_launch(launch, 0, t4a::kTransposeBlock, 0);
     return ok();
   }
   // One matrix's tiles stride over x; the batch is the z coordinate, as in the
   // reference grid (the kernel reads the batch count from nowhere else).
   const t4a::TransposeTiling tiling = t4a::transpose_tiling(dst_fast_extent, src_fast_extent, 1, es);
-  set_launch(launch, blocks_for(tiling.total, 1), kBlock, 0);
+  set_launch(launch, blocks_for(tiling.total, 1), t4a::kTransposeBlock, 0);
   launch->grid[2] = static_cast<unsigned>(batches);
   return ok();
 }
