@@ -268,6 +268,7 @@ struct ReduceDims {
   long long axis_len;
   long long axis_stride;
   long long out_axis_stride;  // partials stride of the split coordinate
+  bool narrow;                // the product of ext[] is below 2^32
 };
 
 T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
@@ -297,6 +298,14 @@ T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
     r->is[r->n] = s;
     r->os[r->n] = o;
     ++r->n;
+  }
+  unsigned long long total = 1;
+  r->narrow = true;
+  for (int k = 0; k < r->n; ++k) {
+    const unsigned long long e = static_cast<unsigned long long>(r->ext[k]);
+    if (e != 0 && total > 0xffffffffull / e) r->narrow = false;
+    total *= e;
+    if (total > 0xffffffffull) r->narrow = false;
   }
 }
 

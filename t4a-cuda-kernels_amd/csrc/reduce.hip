@@ -68,12 +68,21 @@ __device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
                                               long long* in_base, long long* out_off) {
   long long ib = rd.in_offset;
   long long ob = rd.out_offset;
+  // Quotients in 32 bits when every output index fits (rd.narrow: the extent
+  // product is below 2^32); AMD GPUs have no integer divide, and a 64-bit one
+  // costs several times a 32-bit one.
+  const bool narrow = rd.narrow;
+  unsigned int o32 = static_cast<unsigned int>(o);
 #pragma unroll
   for (int k = 0; k < kMaxDims; ++k) {
     if (k >= rd.n) break;
     long long c;
     if (k + 1 == rd.n) {
-      c = o;
+      c = narrow ? static_cast<long long>(o32) : o;
+    } else if (narrow) {
+      const unsigned int e = static_cast<unsigned int>(rd.ext[k]);
+      c = o32 % e;
+      o32 /= e;
     } else {
       const long long e = rd.ext[k];
       c = o % e;
@@ -422,14 +431,18 @@ __device__ __forceinline__ void partials_planes(void* partials_ptr, const void* 
   }
 }
 
-// Unit `u` of the COLUMNS/ROWS mappings: column block fastest, then the other
-// non-axis coordinates, then the split.
+// Unit `u` of the COLUMNS/ROWS mappings: column block fastest, then the split,
+// then the other non-axis coordinates -- neighbouring wavefronts read
+// neighbouring columns of the same rows, or the next chunk of the same columns.
 __device__ __forceinline__ void decode_unit(const PartialsPlan& pp, long long u, long long col,
-                                            long long* ib, long long* pb, long long* split) {
+                                            long long* ib, long long* pb, long long* split,
+                                            long long splits) {
   const ReduceDims& rd = pp.dims;
-  long long rest = u / pp.col_blocks;
-  long long other = rest % pp.others;
-  *split = rest / pp.others;
+  // Every quantity here is below the unit count, which the planner keeps
+  // below 2^31: 32-bit quotients.
+  const unsigned int rest = static_cast<unsigned int>(u) / static_cast<unsigned int>(pp.col_blocks);
+  *split = rest % static_cast<unsigned int>(splits);
+  unsigned int other = rest / static_cast<unsigned int>(splits);
   long long in_base = rd.in_offset;
   long long p_base = rd.out_offset + *split * rd.out_axis_stride;
 #pragma unroll
@@ -439,8 +452,9 @@ __device__ __forceinline__ void decode_unit(const PartialsPlan& pp, long long u,
     if (k == pp.col_dim) {
       c = col;
     } else {
-      c = other % rd.ext[k];
-      other /= rd.ext[k];
+      const unsigned int e = static_cast<unsigned int>(rd.ext[k]);
+      c = other % e;
+      other /= e;
     }
     in_base += c * rd.is[k];
     p_base += c * rd.os[k];
@@ -467,7 +481,7 @@ __device__ __forceinline__ void partials_columns(void* partials_ptr, const void*
     const long long col = (u % pp.col_blocks) * kWave + t;
     if (col >= pp.columns) continue;
     long long ib, pb, split;
-    decode_unit(pp, u, col, &ib, &pb, &split);
+    decode_unit(pp, u, col, &ib, &pb, &split, splits);
     const long long start = split * chunk_len;
     const long long end = split + 1 == splits ? rd.axis_len : start + chunk_len;
     const T* x = in + ib;
@@ -511,14 +525,49 @@ __device__ __forceinline__ void partials_rows(void* partials_ptr, const void* in
   for (long long u = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
        u < pp.units; u += nwaves) {
     long long ib, pb, split;
-    decode_unit(pp, u, c, &ib, &pb, &split);
+    decode_unit(pp, u, c, &ib, &pb, &split, splits);
     const long long start = split * chunk_len;
     const long long len = (split + 1 == splits ? rd.axis_len : start + chunk_len) - start;
     const T* x = in + ib + start * stride;
+    // U row-steps of loads (16 per lane) are issued before they are folded;
+    // each plane lane still folds its rows in increasing order, the first
+    // step seeding (chunks hold at least 32 rows, so step 0 is whole).
+    constexpr int U = A >= 16 ? 1 : 16 / A;
     T acc[A];
+    {
+      T v[U][A];
 #pragma unroll
-    for (int a = 0; a < A; ++a) acc[a] = f.seed(x[(ro + P * a) * stride]);
-    long long q0 = kWarp;
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int a = 0; a < A; ++a) {
+          const long long q = u * kWarp + ro + P * a;
+          if (u == 0 || q < len) v[u][a] = x[q * stride];
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < A; ++a) acc[a] = f.seed(v[0][a]);
+#pragma unroll
+      for (int u = 1; u < U; ++u) {
+#pragma unroll
+        for (int a = 0; a < A; ++a) {
+          if (u * kWarp + ro + P * a < len) acc[a] = f.fold(acc[a], v[u][a]);
+        }
+      }
+    }
+    long long q0 = U * kWarp;
+    for (; q0 + U * kWarp <= len; q0 += U * kWarp) {
+      T v[U][A];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int a = 0; a < A; ++a) v[u][a] = x[(q0 + u * kWarp + ro + P * a) * stride];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int a = 0; a < A; ++a) acc[a] = f.fold(acc[a], v[u][a]);
+      }
+    }
     for (; q0 + kWarp <= len; q0 += kWarp) {
       T v[A];
 #pragma unroll
