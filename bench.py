@@ -13,9 +13,12 @@ step.
 Effective bytes = logical input bytes read once + logical output bytes written
 once (partials excluded), 1 GB = 1e9 B. `roofline` is the dominant kernel's
 algorithmic bytes per launch over its average launch time, measured here with
-HIP events on the launch stream, against the 8 TB/s HBM peak. `cpu_baseline` is
-the CPU oracle (the reference algorithm restated in C, one thread) on a bounded
-sample of the same workload.
+HIP events on the launch stream, against the 8 TB/s HBM peak; `traffic` is that
+kernel's HBM bytes per launch from rocprofv3 FETCH_SIZE and WRITE_SIZE passes
+(`--kernel-only`), each scaled by what the counter reads for copy_exact of a
+known size, recorded in TRAFFIC below. `cpu_baseline` is the CPU oracle (the
+reference algorithm restated in C, one thread) running whole steps of the same
+workload on the same inputs, repeated for about `--cpu-seconds`.
 
 Other workloads (--workload c1|c1big|c3|c4|c5) run the other BASELINE configs
 the same way; they are for development, the driver's line is c2.
@@ -43,6 +46,27 @@ from t4a_cuda_kernels import hip, hipmem  # noqa: E402
 HBM_PEAK_GBPS = 8000.0
 ROTATE = 3
 
+# HBM bytes per launch of a workload's dominant kernel, from two rocprofv3 --pmc
+# passes over `bench.py --workload W --kernel-only OP` (FETCH_SIZE, then
+# WRITE_SIZE, KiB per dispatch averaged over the launches), each multiplied by
+# the copy calibration: copy_exact of 256 MiB reads and writes 268435456 bytes,
+# and the factor is that over what the counter reports for it. A kernel change
+# needs a new measurement; until then the entry is left out and traffic is null.
+TRAFFIC: dict[tuple[str, str], dict] = {
+    ("c2", "sum_i64_inner"): {"bytes": 542151847,
+                              "source": "profiles/reduce_partials_c2_traffic.md"},
+}
+
+NUMPY_DTYPE = {t.DType.F32: np.float32, t.DType.F64: np.float64, t.DType.I32: np.int32,
+               t.DType.I64: np.int64, t.DType.Bool: np.uint8, t.DType.C32: np.complex64,
+               t.DType.C64: np.complex128}
+
+
+def _oracle():
+    """The CPU oracle, imported only by the cpu_baseline leg."""
+    from oracle import t4a_oracle as orc
+    return orc
+
 
 @dataclass
 class Op:
@@ -54,7 +78,7 @@ class Op:
     launch: Callable[[int], None]    # enqueue the op on buffer set r
     dominant: Callable[[int], None]  # enqueue only the dominant kernel
     dominant_bytes: int              # algorithmic bytes of the dominant kernel
-    cpu: Callable[[], float] | None = None  # CPU oracle on a sample; returns bytes
+    cpu: Callable[[], None] | None = None  # the same op through the CPU oracle
 
 
 @dataclass
@@ -90,8 +114,9 @@ def _empty_like(bufs) -> list:
     return [hipmem.DeviceBuffer(b.nbytes) for b in bufs]
 
 
-def reduction_op(name, dtype, op, in_ext, axis, sets, cpu_sample=None) -> Op:
-    """A planned reduction over compact `in_ext` (reference axis order)."""
+def reduction_op(name, dtype, op, in_ext, axis, sets, host) -> Op:
+    """A planned reduction over compact `in_ext` (reference axis order); `host`
+    is the input's host copy, which the CPU leg reduces with the same plan."""
     in_l = t.Layout.compact(in_ext)
     oe = list(in_ext)
     oe[axis] = 1
@@ -118,12 +143,33 @@ def reduction_op(name, dtype, op, in_ext, axis, sets, cpu_sample=None) -> Op:
             hip.reduce(out, sets[r], dtype, op, plan.strategy, out_l, in_l, axis, on,
                        plan.launch, _stream())
 
+    host_bufs = {}
+
+    def cpu():
+        orc = _oracle()
+        if not host_bufs:
+            host_bufs["out"] = np.zeros(on, dtype=NUMPY_DTYPE[dtype])
+            if pl is not None:
+                host_bufs["part"] = np.zeros(pl.element_count(), dtype=NUMPY_DTYPE[dtype])
+        h_out = host_bufs["out"]
+        if plan.kind == "Split":
+            h_part = host_bufs["part"]
+            orc.reduce_partials(h_part, host, dtype, op, 32, pl, in_l, axis, on,
+                                plan.split.splits, plan.split.chunk_len)
+            width = (plan.pass2.block[0] if plan.combine_strategy == t.ReduceStrategy.Plane
+                     else 32)
+            orc.reduce(h_out, h_part, dtype, plan.combine_op, plan.combine_strategy, width,
+                       out_l, pl, axis, on)
+        else:
+            width = plan.launch.block[0] if plan.strategy == t.ReduceStrategy.Plane else 32
+            orc.reduce(h_out, host, dtype, op, plan.strategy, width, out_l, in_l, axis, on)
+
     kernel = "reduce_partials" if plan.kind == "Split" else "reduce"
-    return Op(name, kernel, (n + on) * es, launch, dominant, (n + (pl.element_count() if pl else on)) * es,
-              cpu_sample)
+    return Op(name, kernel, (n + on) * es, launch, dominant,
+              (n + (pl.element_count() if pl else on)) * es, cpu)
 
 
-def transpose_op(name, dtype, m, n, sets, outs) -> Op:
+def transpose_op(name, dtype, m, n, sets, outs, host) -> Op:
     plan = t.plan_tiled_transpose(dtype, t.TransposeConfig.DEFAULT, 0, m * n, m, n, 1, m * n,
                                   m * n)
     cfg = t.TransposeConfig.DEFAULT
@@ -131,11 +177,18 @@ def transpose_op(name, dtype, m, n, sets, outs) -> Op:
     def launch(r):
         hip.tiled_transpose(outs[r], sets[r], dtype, 0, m * n, m, n, cfg, plan, _stream())
 
+    h_dst = []
+
+    def cpu():
+        if not h_dst:
+            h_dst.append(np.empty_like(host))
+        _oracle().tiled_transpose(h_dst[0], host, dtype, 0, m * n, m, n, 1)
+
     return Op(name, "tiled_transpose", 2 * m * n * dtype.size, launch, launch,
-              2 * m * n * dtype.size)
+              2 * m * n * dtype.size, cpu)
 
 
-def move_op(name, dtype, src_l, dst_l, sets, outs) -> Op:
+def move_op(name, dtype, src_l, dst_l, sets, outs, host) -> Op:
     count = src_l.element_count()
     src_len = src_l.max_reachable_offset() + 1
     dst_len = dst_l.max_reachable_offset() + 1
@@ -144,60 +197,41 @@ def move_op(name, dtype, src_l, dst_l, sets, outs) -> Op:
     def launch(r):
         hip.strided_to_strided(outs[r], sets[r], dtype, src_l, dst_l, count, plan, _stream())
 
+    h_dst = []
+
+    def cpu():
+        if not h_dst:
+            h_dst.append(np.empty(dst_len * dtype.size, dtype=np.uint8))
+        _oracle().strided_to_strided(h_dst[0], host, dtype, src_l, dst_l, count)
+
     return Op(name, "strided_to_strided", 2 * count * dtype.size, launch, launch,
-              2 * count * dtype.size)
+              2 * count * dtype.size, cpu)
 
 
 # ---- workloads ---------------------------------------------------------------------
-
-def cpu_c2_sample():
-    """Oracle: f32 sum over the inner axis of a 1024-row slice of C2, plus the
-    same slice's outer-axis sum (one thread)."""
-    from oracle import t4a_oracle as orc
-
-    rng = np.random.default_rng(1)
-    rows = 1024
-    x = rng.uniform(-1, 1, 8192 * rows).astype(np.float32)
-    moved = 0
-    for axis, ext in ((0, [8192, rows]), (1, [8192, rows])):
-        in_l = t.Layout.compact(ext)
-        oe = list(ext)
-        oe[axis] = 1
-        out_l = t.Layout.compact(oe)
-        on = out_l.element_count()
-        plan = t.plan_reduction(t.DType.F32, t.ReduceOp.Sum, out_l, on, in_l, x.size, axis, 32)
-        pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
-        part = np.zeros(pl.element_count(), dtype=np.float32)
-        out = np.zeros(on, dtype=np.float32)
-        orc.reduce_partials(part, x, t.DType.F32, t.ReduceOp.Sum, 32, pl, in_l, axis, on,
-                            plan.split.splits, plan.split.chunk_len)
-        orc.reduce(out, part, t.DType.F32, t.ReduceOp.Sum, plan.combine_strategy, 32, out_l, pl,
-                   axis, on)
-        moved += (x.size + on) * 4
-    return moved
-
 
 def build_c2() -> Workload:
     w = Workload("c2", "C2: f32 [8192,8192] sum+max over inner and outer axis, i64 [8192,8192] "
                  "sum over the inner axis (planned split reductions)", "f32,i64")
     ext = [8192, 8192]  # C-shape [8192, 8192]: reference axis 0 is the inner one
     rng = np.random.default_rng(1)
-    f = _sets(rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32))
-    i64 = _sets(rng.integers(-1000, 1001, 8192 * 8192, dtype=np.int64))
-    w.ops.append(reduction_op("sum_f32_inner", t.DType.F32, t.ReduceOp.Sum, ext, 0, f,
-                              cpu_c2_sample))
-    w.ops.append(reduction_op("max_f32_inner", t.DType.F32, t.ReduceOp.Max, ext, 0, f))
-    w.ops.append(reduction_op("sum_f32_outer", t.DType.F32, t.ReduceOp.Sum, ext, 1, f))
-    w.ops.append(reduction_op("max_f32_outer", t.DType.F32, t.ReduceOp.Max, ext, 1, f))
-    w.ops.append(reduction_op("sum_i64_inner", t.DType.I64, t.ReduceOp.Sum, ext, 0, i64))
+    hf = rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32)
+    hi = rng.integers(-1000, 1001, 8192 * 8192, dtype=np.int64)
+    f, i64 = _sets(hf), _sets(hi)
+    w.ops.append(reduction_op("sum_f32_inner", t.DType.F32, t.ReduceOp.Sum, ext, 0, f, hf))
+    w.ops.append(reduction_op("max_f32_inner", t.DType.F32, t.ReduceOp.Max, ext, 0, f, hf))
+    w.ops.append(reduction_op("sum_f32_outer", t.DType.F32, t.ReduceOp.Sum, ext, 1, f, hf))
+    w.ops.append(reduction_op("max_f32_outer", t.DType.F32, t.ReduceOp.Max, ext, 1, f, hf))
+    w.ops.append(reduction_op("sum_i64_inner", t.DType.I64, t.ReduceOp.Sum, ext, 0, i64, hi))
     return w
 
 
 def build_c1(m: int) -> Workload:
     w = Workload(f"c1-{m}", f"C1: tiled transpose f32 [{m},{m}] (1,0)", "f32")
-    sets = _sets(np.random.default_rng(0).uniform(-1.0, 1.0, m * m).astype(np.float32))
+    host = np.random.default_rng(0).uniform(-1.0, 1.0, m * m).astype(np.float32)
+    sets = _sets(host)
     outs = _empty_like(sets)
-    w.ops.append(transpose_op(f"transpose_f32_{m}", t.DType.F32, m, m, sets, outs))
+    w.ops.append(transpose_op(f"transpose_f32_{m}", t.DType.F32, m, m, sets, outs, host))
     return w
 
 
@@ -208,9 +242,10 @@ def build_c3() -> Workload:
     dst_l = t.Layout.compact([64, 64, 128, 32])
     rng = np.random.default_rng(2)
     for dt in (t.DType.F64, t.DType.C32):
-        sets = _sets(rng.standard_normal(16777216 * dt.size // 8))
+        host = rng.standard_normal(16777216 * dt.size // 8)
+        sets = _sets(host)
         outs = _empty_like(sets)
-        w.ops.append(move_op(f"permute4_{dt.name}", dt, src_l, dst_l, sets, outs))
+        w.ops.append(move_op(f"permute4_{dt.name}", dt, src_l, dst_l, sets, outs, host))
     return w
 
 
@@ -219,11 +254,13 @@ def build_c4() -> Workload:
                  "over the last axis", "f32,i32")
     ext = [4, 1048576, 32]
     rng = np.random.default_rng(3)
-    f = _sets(rng.standard_normal(4 * 1048576 * 32).astype(np.float32))
-    i32 = _sets(rng.choice(np.array([-1, 1, 2], dtype=np.int32), 4 * 1048576 * 32))
-    w.ops.append(reduction_op("sumsq_f32_middle", t.DType.F32, t.ReduceOp.SumSquares, ext, 1, f))
-    w.ops.append(reduction_op("min_f32_middle", t.DType.F32, t.ReduceOp.Min, ext, 1, f))
-    w.ops.append(reduction_op("prod_i32_last", t.DType.I32, t.ReduceOp.Prod, ext, 0, i32))
+    hf = rng.standard_normal(4 * 1048576 * 32).astype(np.float32)
+    hi = rng.choice(np.array([-1, 1, 2], dtype=np.int32), 4 * 1048576 * 32)
+    f, i32 = _sets(hf), _sets(hi)
+    w.ops.append(reduction_op("sumsq_f32_middle", t.DType.F32, t.ReduceOp.SumSquares, ext, 1, f,
+                              hf))
+    w.ops.append(reduction_op("min_f32_middle", t.DType.F32, t.ReduceOp.Min, ext, 1, f, hf))
+    w.ops.append(reduction_op("prod_i32_last", t.DType.I32, t.ReduceOp.Prod, ext, 0, i32, hi))
     return w
 
 
@@ -231,11 +268,14 @@ def build_c5() -> Workload:
     w = Workload("c5", "C5: c64 [16]^6 permute (5,2,0,4,1,3) then sum over C-axis 3", "c64")
     src_l = t.Layout([16] * 6, [256, 65536, 16, 1048576, 4096, 1], 0)
     dst_l = t.Layout.compact([16] * 6)
-    sets = _sets(np.random.default_rng(4).standard_normal(16 ** 6 * 2))
+    host = np.random.default_rng(4).standard_normal(16 ** 6 * 2)
+    sets = _sets(host)
     outs = _empty_like(sets)
-    w.ops.append(move_op("permute6_c64", t.DType.C64, src_l, dst_l, sets, outs))
-    # the sum reads the permuted (compact) tensor
-    w.ops.append(reduction_op("sum_c64_axis3", t.DType.C64, t.ReduceOp.Sum, [16] * 6, 2, outs))
+    w.ops.append(move_op("permute6_c64", t.DType.C64, src_l, dst_l, sets, outs, host))
+    # the sum reads the permuted (compact) tensor; the CPU leg reduces a tensor of
+    # the same shape (the source), which is the same work
+    w.ops.append(reduction_op("sum_c64_axis3", t.DType.C64, t.ReduceOp.Sum, [16] * 6, 2, outs,
+                              host))
     return w
 
 
@@ -286,6 +326,11 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="repeat whole CPU steps until this much time has passed")
+    ap.add_argument("--kernel-only", metavar="OP",
+                    help="launch only OP's dominant kernel, warmup + steps times (for "
+                         "rocprofv3 counter passes), and print one line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
@@ -296,6 +341,20 @@ def main() -> None:
         sys.exit(2)
 
     w = WORKLOADS[args.workload]()
+    if args.kernel_only:
+        ops = {op.name: op for op in w.ops}
+        if args.kernel_only not in ops:
+            print(f"no op {args.kernel_only!r} in workload {w.name}: {sorted(ops)}",
+                  file=sys.stderr)
+            sys.exit(2)
+        op = ops[args.kernel_only]
+        for i in range(args.warmup + args.steps):
+            op.dominant(i % ROTATE)
+        _stream().synchronize()
+        print(json.dumps({"kernel_only": op.name, "workload": w.name, "kernel": op.kernel,
+                          "launches": args.warmup + args.steps,
+                          "algorithmic_bytes": op.dominant_bytes}))
+        return
     step = lambda r: [op.launch(r) for op in w.ops]  # noqa: E731
     for i in range(args.warmup):
         step(i % ROTATE)
@@ -318,20 +377,34 @@ def main() -> None:
             dom = (op, k_ms)
     op, k_ms = dom
     achieved = op.dominant_bytes / (k_ms * 1e-3) / 1e9
+    measured = TRAFFIC.get((w.name, op.name))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": measured["bytes"] if measured else None,
+                "algorithmic_bytes": op.dominant_bytes,
                 "kernel": f"{op.kernel} ({op.name})", "kernel_ms": round(k_ms, 5)}
+    if measured:
+        roofline["traffic_source"] = measured["source"]
 
     cpu = None
     cpu_ops = [o for o in w.ops if o.cpu is not None]
     if cpu_ops and not args.no_cpu:
-        t0 = time.perf_counter()
-        moved = cpu_ops[0].cpu()
-        dt = time.perf_counter() - t0
+        # whole steps of the same workload on the same inputs, until the budget is spent
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            for o in cpu_ops:
+                o.cpu()
+            steps += 1
+            dt = time.perf_counter() - t0
+            if dt >= args.cpu_seconds or steps >= 100:
+                break
+        moved = steps * sum(o.algo_bytes for o in cpu_ops)
+        names = ", ".join(o.name for o in cpu_ops)
         cpu = {"value": round(moved / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "CPU oracle (reference topology restated in C, 1 thread): f32 sum "
-                         "over the inner and the outer axis of a [1024, 8192] slice of C2, "
-                         "pass 1 + combine", "seconds": round(dt, 3)}
+               "sample": f"CPU oracle (the reference's algorithm and fold topology restated in "
+                         f"C, one thread), {steps} whole step(s) of workload {w.name} ({names}) "
+                         f"on the same full-size inputs, same effective-byte count",
+               "seconds": round(dt, 2), "steps": steps}
 
     print(json.dumps({
         "metric": "effective GB/s + % HBM roofline: transpose, strided permute, axis reduce",
