@@ -4,6 +4,12 @@ Run `python t4a-cuda-kernels_amd/build.py` (or `__graft_entry__.build()`). The
 shared library is written next to the Python package
 (`t4a_cuda_kernels/libt4a_hip.so`) so that it travels with the source tree.
 
+Each HIP source is also built as a standalone gfx950 code object
+(`t4a_cuda_kernels/t4a_movement.gfx950.hsaco`, `t4a_reduce.gfx950.hsaco`) that
+exports the reference's kernel entry names, for callers that load kernels by
+name from a module (`hipModuleLoadData` + `hipModuleGetFunction`), as the
+reference's callers do with its cubins.
+
 HIP sources are compiled for gfx950 only, with:
   -ffp-contract=off      every floating-point rounding is the one written
                          (the fold topology and the complex product spell
@@ -28,6 +34,10 @@ ARCH = "gfx950"
 
 HIP_SOURCES = ["movement.hip", "reduce.hip"]
 CXX_SOURCES = ["planner.cpp"]
+
+
+def code_object_name(source: str) -> str:
+    return f"t4a_{Path(source).stem}.{ARCH}.hsaco"
 
 
 def _hipcc() -> str:
@@ -65,18 +75,20 @@ def build(verbose: bool = False) -> Path:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
     ]
+    OUT_DIR.mkdir(exist_ok=True)
     hip_cmds = []
     for src in HIP_SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         hip_cmds.append([hipcc, *hip_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)])
         objects.append(obj)
+        hip_cmds.append([hipcc, "--genco", "--no-gpu-bundle-output", *hip_flags, *includes,
+                         str(CSRC / src), "-o", str(OUT_DIR / code_object_name(src))])
     # The translation units are independent: compile them side by side.
     with ThreadPoolExecutor(max_workers=len(hip_cmds)) as pool:
         for cmd in hip_cmds:
             if verbose:
                 print(" ".join(cmd))
         list(pool.map(_run, hip_cmds))
-    OUT_DIR.mkdir(exist_ok=True)
     out = OUT_DIR / LIB_NAME
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects),

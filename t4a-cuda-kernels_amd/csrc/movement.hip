@@ -57,9 +57,14 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
   const long long b = blockIdx.z;
   const P* s = src + src_offset + b * S;
   P* d = dst + b * S;
-  const int tid = threadIdx.x;
-  const int nthreads = blockDim.x;
-  for (long long t = blockIdx.x; t < per_batch; t += gridDim.x) {
+  // Threads and blocks are numbered flat over x and y, so the reference's 2-D
+  // geometry (grid (tiles of M, tiles of N, batches), block (tile / vw, rows))
+  // and this build's 1-D persistent one both cover every tile exactly once.
+  const int tid = threadIdx.x + threadIdx.y * blockDim.x;
+  const int nthreads = blockDim.x * blockDim.y;
+  const long long nblocks = static_cast<long long>(gridDim.x) * gridDim.y;
+  for (long long t = blockIdx.x + static_cast<long long>(blockIdx.y) * gridDim.x;
+       t < per_batch; t += nblocks) {
     const long long tm = t % tiles_m;
     const long long tn = (t / tiles_m + tm) % tiles_n;
     const long long i0 = tm * TM;

@@ -43,6 +43,13 @@ def hip() -> ctypes.CDLL:
         lib.hipEventSynchronize.argtypes = [c_void_p]
         lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(c_float), c_void_p, c_void_p]
         lib.hipDeviceGetName.argtypes = [ctypes.c_char_p, c_int, c_int]
+        lib.hipModuleLoadData.argtypes = [ctypes.POINTER(c_void_p), c_void_p]
+        lib.hipModuleUnload.argtypes = [c_void_p]
+        lib.hipModuleGetFunction.argtypes = [ctypes.POINTER(c_void_p), c_void_p, ctypes.c_char_p]
+        lib.hipModuleLaunchKernel.argtypes = [c_void_p, ctypes.c_uint, ctypes.c_uint,
+                                              ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                              ctypes.c_uint, ctypes.c_uint, c_void_p,
+                                              ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]
         _HIP = lib
     return _HIP
 
@@ -174,5 +181,48 @@ class Event:
         try:
             if self.handle:
                 hip().hipEventDestroy(c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+class Module:
+    """A loaded gfx950 code object whose kernels are found by name, as the
+    reference's callers load its cubins (reference tests/gpu/mod.rs:81-111)."""
+
+    def __init__(self, path):
+        self._image = ctypes.create_string_buffer(open(path, "rb").read())
+        m = c_void_p()
+        check(hip().hipModuleLoadData(byref(m), ctypes.cast(self._image, c_void_p)),
+              f"hipModuleLoadData({path})")
+        self.handle = m.value
+        self._functions: dict[str, int] = {}
+
+    def function(self, name: str) -> int:
+        if name not in self._functions:
+            f = c_void_p()
+            check(hip().hipModuleGetFunction(byref(f), c_void_p(self.handle), name.encode()),
+                  f"hipModuleGetFunction({name})")
+            self._functions[name] = f.value
+        return self._functions[name]
+
+    def launch(self, name: str, grid, block, shared_bytes: int, stream, args) -> None:
+        """Launch `name` with `kernelParams` pointing at each ctypes argument in
+        `args` (by-value structs included); an empty grid launches nothing."""
+        if 0 in tuple(grid):
+            return
+        params = (c_void_p * len(args))(*[ctypes.cast(byref(a), c_void_p) for a in args])
+        s = c_void_p(stream.handle if isinstance(stream, Stream) else (stream or 0))
+        check(hip().hipModuleLaunchKernel(c_void_p(self.function(name)), *map(int, grid),
+                                          *map(int, block), int(shared_bytes), s, params, None),
+              f"hipModuleLaunchKernel({name})")
+
+    def unload(self) -> None:
+        if getattr(self, "handle", None):
+            hip().hipModuleUnload(c_void_p(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.unload()
         except Exception:
             pass

@@ -49,6 +49,22 @@ def test_library_exports_the_reference_kernel_entries():
         assert hasattr(lib, name), name
 
 
+def test_code_objects_export_the_reference_kernel_entries():
+    """The gfx950 code objects a module-loading caller finds kernels in by name."""
+    readelf = Path("/opt/rocm/llvm/bin/llvm-readelf")
+    pkg = Path(_lib.LIB_PATH).parent
+    wanted = {"t4a_movement.gfx950.hsaco": KERNEL_SYMBOLS[:4],
+              "t4a_reduce.gfx950.hsaco": KERNEL_SYMBOLS[4:]}
+    for name, symbols in wanted.items():
+        path = pkg / name
+        assert path.exists(), f"{name} not built"
+        syms = subprocess.run([str(readelf), "--syms", "--wide", str(path)], capture_output=True,
+                              text=True, check=True).stdout
+        for sym in symbols:
+            assert re.search(rf"FUNC\s+GLOBAL\s+\S+\s+\S+\s+{sym}$", syms, re.M), (name, sym)
+            assert re.search(rf"OBJECT\s+GLOBAL\s+\S+\s+\S+\s+{sym}\.kd$", syms, re.M), (name, sym)
+
+
 def test_headers_compile_as_c_and_cxx(tmp_path):
     src = tmp_path / "probe.c"
     src.write_text('#include "t4a/abi.h"\n#include "t4a/t4a.h"\n'
