@@ -18,6 +18,20 @@
 
 namespace t4a {
 
+// Threads per block: the launcher's compile-time block size BS, or, for BS = 0
+// (the geometry-agnostic reference entries), blockDim.x. blockDim is an
+// implicit kernel argument that a wavefront fetches with a vector memory load,
+// so a short-lived wavefront that reads it waits one memory round trip before
+// its first data load; a constant costs nothing.
+template <int BS>
+__device__ __forceinline__ int block_threads() {
+  if constexpr (BS > 0) {
+    return BS;
+  } else {
+    return static_cast<int>(blockDim.x);
+  }
+}
+
 using c32 = t4a_cuda_c32;
 using c64 = t4a_cuda_c64;
 
@@ -118,6 +132,22 @@ __device__ __forceinline__ double vmax<double>(double a, double b) { return fmax
 template <>
 __device__ __forceinline__ double vmin<double>(double a, double b) { return fmin_nan(a, b); }
 
+// IEEE 754-2019 maximum / minimum: NaN-propagating, -0 below +0
+// (v_maximum3_f32 / v_minimum3_f32 on gfx950, three operands per instruction).
+// Among non-NaN operands the select-form extrema above pick the same bits in any
+// order (equal values AND / OR their bits, which orders -0 below +0), so a Max
+// or Min fold without a NaN may take any order through these; a NaN result
+// sends the caller back to the select form, whose NaN choice is
+// order-dependent.
+template <typename T>
+__device__ __forceinline__ T ieee_maximum(T a, T b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+template <typename T>
+__device__ __forceinline__ T ieee_minimum(T a, T b) {
+  return __builtin_elementwise_minimum(a, b);
+}
+
 // ---- folds ---------------------------------------------------------------------
 // seed(v): the accumulator's first value; fold(acc, v): one more element;
 // combine(a, b): two accumulators. Only SUM_SQUARES tells fold and combine apart
@@ -179,6 +209,26 @@ __device__ __forceinline__ T plane_tree(T v, int width, Fold f) {
   for (int off = 1; off < width; off <<= 1) v = f.combine(v, shfl_xor(v, off, width));
   return v;
 }
+
+// The any-order twin of a float Max / Min fold (see ieee_maximum), or void.
+template <typename Fold, typename T>
+struct AnyOrder {
+  using type = void;
+};
+struct AnyOrderMax {
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const {
+    return ieee_maximum(a, b);
+  }
+};
+struct AnyOrderMin {
+  template <typename T> __device__ __forceinline__ T combine(T a, T b) const {
+    return ieee_minimum(a, b);
+  }
+};
+template <> struct AnyOrder<MaxFold, float> { using type = AnyOrderMax; };
+template <> struct AnyOrder<MaxFold, double> { using type = AnyOrderMax; };
+template <> struct AnyOrder<MinFold, float> { using type = AnyOrderMin; };
+template <> struct AnyOrder<MinFold, double> { using type = AnyOrderMin; };
 
 // Pairwise own-left tree over `n` register values (n a power of two); the
 // value of lane 0 of a plane whose lanes are held by one thread.

@@ -309,6 +309,38 @@ T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
   }
 }
 
+// Division of x < 2^31 by an invariant d >= 1 as a multiply-high, an add and a
+// shift (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, section 4): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, q = (mulhi(m, x) + x) >> l; x < 2^31 keeps
+// the sum inside 32 bits. AMD GPUs have no integer divide instruction: a
+// runtime 32-bit division is a dozen dependent instructions.
+struct FastDiv {
+  unsigned int d;
+  unsigned int m;
+  int shift;
+};
+
+T4A_HD FastDiv fast_div(unsigned int d) {
+  FastDiv f;
+  f.d = d;
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  f.shift = l;
+  f.m = static_cast<unsigned int>((((1ull << l) - d) << 32) / d + 1);
+  return f;
+}
+
+T4A_HD unsigned int div_by(unsigned int x, const FastDiv& f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned int t = __umulhi(f.m, x);
+#else
+  const unsigned int t =
+      static_cast<unsigned int>((static_cast<unsigned long long>(f.m) * x) >> 32);
+#endif
+  return (t + x) >> f.shift;
+}
+
 // Element types the sideways pass-1 mappings serve (real and integer; complex
 // keeps the plane mapping).
 T4A_HD bool sideways_dtype(int dtype) {
@@ -394,6 +426,56 @@ T4A_HD bool stream_applies(const PartialsPlan& p, int dtype, int op, long long c
     if (p.dims.is[k] % v != 0) return false;
   }
   return true;
+}
+
+// Batch slots (groups per lane, 1..4) of the lean pass-1 mapping, or 0 where it
+// does not apply: the streaming conditions above, and the longest chunk (the
+// last one, which absorbs the remainder) holding at most 4 * 32 groups, so each
+// lane's share is the grouped walk's first batch alone.
+T4A_HD int lean_slots(const PartialsPlan& p, int dtype, int op, long long splits,
+                      long long chunk_len, int plane_width) {
+  if (!stream_applies(p, dtype, op, chunk_len, plane_width)) return 0;
+  // The lean plan's decode: at most three fused non-axis dims, cube and output
+  // indices below 2^31 (32-bit quotients).
+  if (p.dims.n > 3 || p.units >= (1ll << 31)) return 0;
+  const long long v = 16 / dtype_size(dtype);
+  const long long last = p.dims.axis_len - (splits - 1) * chunk_len;
+  const long long slots = (last / v + kWarp - 1) / kWarp;
+  return slots <= 4 ? static_cast<int>(slots) : 0;
+}
+
+// The lean mapping's own plan: the fused non-axis dims (at most three) with
+// their divisors precomputed, and the split walk.
+struct LeanPlan {
+  long long in_offset;
+  long long out_offset;
+  long long is[3];
+  long long os[3];
+  FastDiv ext[3];
+  FastDiv splits;
+  int n;
+  int last_len;
+  long long chunk_len;
+  long long out_axis_stride;
+};
+
+T4A_HD LeanPlan lean_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
+  LeanPlan lp;
+  const ReduceDims& rd = p.dims;
+  lp.in_offset = rd.in_offset;
+  lp.out_offset = rd.out_offset;
+  lp.n = rd.n;
+  for (int k = 0; k < 3; ++k) {
+    const bool used = k < rd.n;
+    lp.is[k] = used ? rd.is[k] : 0;
+    lp.os[k] = used ? rd.os[k] : 0;
+    lp.ext[k] = fast_div(used ? static_cast<unsigned int>(rd.ext[k]) : 1u);
+  }
+  lp.splits = fast_div(static_cast<unsigned int>(splits));
+  lp.last_len = static_cast<int>(rd.axis_len - (splits - 1) * chunk_len);
+  lp.chunk_len = chunk_len;
+  lp.out_axis_stride = rd.out_axis_stride;
+  return lp;
 }
 
 // Cubes each streaming plane takes: enough planes to fill the chip (16384, four

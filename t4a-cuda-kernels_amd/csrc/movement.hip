@@ -362,12 +362,13 @@ __device__ __forceinline__ void move_tiled(void* dst, const void* src, const Mov
 }
 
 // CONTIG: rows along the fused dim `row_dim`, contiguous on both sides.
-template <typename P>
+template <typename P, int BS>
 __device__ __forceinline__ void move_rows(void* dst, const void* src, const MovePlan& p) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
-  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < p.len;
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  for (long long f = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; f < p.len;
        f += gstride) {
     long long rest = f / p.row_len;
     long long so = p.src_offset + (f - rest * p.row_len);
@@ -384,12 +385,13 @@ __device__ __forceinline__ void move_rows(void* dst, const void* src, const Move
 }
 
 // GENERIC: one decode per element on both sides.
-template <typename P>
+template <typename P, int BS>
 __device__ __forceinline__ void move_elements(void* dst, const void* src, const MovePlan& p) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
-  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < p.len;
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  for (long long f = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; f < p.len;
        f += gstride) {
     long long rest = f;
     long long so = p.src_offset;
@@ -409,8 +411,8 @@ __device__ __forceinline__ void move_dispatch(void* dst, const void* src, const 
                                               unsigned char* lds) {
   switch (p.mode) {
     case kMoveTiled: move_tiled<P>(dst, src, p, lds); break;
-    case kMoveContig: move_rows<P>(dst, src, p); break;
-    case kMoveGeneric: move_elements<P>(dst, src, p); break;
+    case kMoveContig: move_rows<P, 0>(dst, src, p); break;
+    case kMoveGeneric: move_elements<P, 0>(dst, src, p); break;
     default: break;
   }
 }
@@ -441,23 +443,24 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
 // buffers, go element by element.
 constexpr int kCopyUnroll = 4;
 
-template <typename P>
+template <typename P, int BS>
 __device__ __forceinline__ void copy_elements(void* dst, const void* src, long long first,
                                               long long len) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
-  for (long long i = first + static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-       i < len; i += gstride)
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  for (long long i = first + static_cast<long long>(blockIdx.x) * bs + threadIdx.x; i < len;
+       i += gstride)
     d[i] = s[i];
 }
 
-template <typename P>
+template <typename P, int BS>
 __device__ __forceinline__ void copy_body(void* dst, const void* src, long long len) {
   const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) &
                         15) == 0;
   if (!aligned || sizeof(P) > 16) {
-    copy_elements<P>(dst, src, 0, len);
+    copy_elements<P, BS>(dst, src, 0, len);
     return;
   }
   // Each block streams one contiguous span of 16-byte vectors, its threads
@@ -469,7 +472,7 @@ __device__ __forceinline__ void copy_body(void* dst, const void* src, long long 
   const long long end = begin + span < vectors ? begin + span : vectors;
   Bits128* d = static_cast<Bits128*>(dst);
   const Bits128* s = static_cast<const Bits128*>(src);
-  const long long step = blockDim.x;
+  const long long step = block_threads<BS>();
   long long i = begin + threadIdx.x;
   for (; i + (kCopyUnroll - 1) * step < end; i += kCopyUnroll * step) {
     V16 v[kCopyUnroll];
@@ -480,15 +483,15 @@ __device__ __forceinline__ void copy_body(void* dst, const void* src, long long 
   }
   for (; i < end; i += step) nt_store<Bits128, 1>(d + i, nt_load<Bits128, 1>(s + i));
   // Elements after the last whole vector.
-  copy_elements<P>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len);
+  copy_elements<P, BS>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len);
 }
 
 // ---- kernels the launchers use: one per payload width, the plan computed on
 // the host and passed by value. ----
 
-template <typename P>
+template <typename P, int BS>
 __global__ void __launch_bounds__(256) copy_kernel(void* dst, const void* src, long long len) {
-  copy_body<P>(dst, src, len);
+  copy_body<P, BS>(dst, src, len);
 }
 
 template <typename P>
@@ -507,12 +510,12 @@ __global__ void __launch_bounds__(256)
   move_tiled_as<P, VL, VS>(dst, src, plan, lds);
 }
 
-template <typename P>
+template <typename P, int BS>
 __global__ void __launch_bounds__(256) move_flat_kernel(void* dst, const void* src, MovePlan plan) {
   if (plan.mode == kMoveContig) {
-    move_rows<P>(dst, src, plan);
+    move_rows<P, BS>(dst, src, plan);
   } else {
-    move_elements<P>(dst, src, plan);
+    move_elements<P, BS>(dst, src, plan);
   }
 }
 
@@ -554,10 +557,10 @@ extern "C" __global__ void __launch_bounds__(512)
 extern "C" __global__ void __launch_bounds__(256)
     t4a_cuda_copy_exact(void* dst, const void* src, int dtype, long long len) {
   switch (t4a::dtype_size(dtype)) {
-    case 1: t4a::copy_body<uint8_t>(dst, src, len); break;
-    case 4: t4a::copy_body<uint32_t>(dst, src, len); break;
-    case 8: t4a::copy_body<unsigned long long>(dst, src, len); break;
-    case 16: t4a::copy_body<t4a::Elem16>(dst, src, len); break;
+    case 1: t4a::copy_body<uint8_t, 0>(dst, src, len); break;
+    case 4: t4a::copy_body<uint32_t, 0>(dst, src, len); break;
+    case 8: t4a::copy_body<unsigned long long, 0>(dst, src, len); break;
+    case 16: t4a::copy_body<t4a::Elem16, 0>(dst, src, len); break;
     default: break;
   }
 }
@@ -626,7 +629,11 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
     if (plan.mode != t4a::kMoveTiled) {
-      hipLaunchKernelGGL(t4a::move_flat_kernel<P>, grid, block, 0, s, dst, src, plan);
+      if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+        hipLaunchKernelGGL((t4a::move_flat_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src,
+                           plan);
+      else
+        hipLaunchKernelGGL((t4a::move_flat_kernel<P, 0>), grid, block, 0, s, dst, src, plan);
       return status_of_last_launch();
     }
     constexpr int V = t4a::tile_vector<P>();
@@ -678,8 +685,11 @@ extern "C" int t4a_hip_copy_exact(void* dst, const void* src, int dtype, long lo
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
-    hipLaunchKernelGGL(t4a::copy_kernel<P>, grid, block, 0, static_cast<hipStream_t>(stream),
-                       dst, src, len);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+      hipLaunchKernelGGL((t4a::copy_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src, len);
+    else
+      hipLaunchKernelGGL((t4a::copy_kernel<P, 0>), grid, block, 0, s, dst, src, len);
     return status_of_last_launch();
   });
 }

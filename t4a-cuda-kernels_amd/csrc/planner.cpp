@@ -504,8 +504,10 @@ int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_
                      split.splits, t4a::kWarp, t4a::sideways_dtype(dtype));
   long long per_block =
       plan.mode == t4a::kPartialsPlane ? kBlock / t4a::kWarp : kBlock / t4a::kWave;
-  if (t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))
-    per_block *= t4a::stream_cubes_per_plane(cubes);  // planes take runs of cubes
+  // Lean planes take one cube each; streaming planes take runs of cubes.
+  if (!t4a::lean_slots(plan, dtype, op, split.splits, split.chunk_len, t4a::kWarp) &&
+      t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))
+    per_block *= t4a::stream_cubes_per_plane(cubes);
   set_launch(launch, plan.units == 0 ? 0 : blocks_for(plan.units, per_block), kBlock, 0);
   return ok();
 }

@@ -99,15 +99,16 @@ __device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
 // One thread per output, serial fold from element 0 (reference reduce.cu:196-224).
 // On a contiguous axis whose every output starts 16-byte aligned, the elements
 // arrive as 16-byte groups; the fold order is unchanged.
-template <typename Fold, typename T, bool Vector>
+template <typename Fold, typename T, bool Vector, int BS>
 __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __restrict__ in,
                                              const ReduceDims& rd, long long output_len,
                                              Fold f) {
   const long long len = rd.axis_len;
   const long long stride = rd.axis_stride;
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
-  for (long long o = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-       o < output_len; o += gstride) {
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  for (long long o = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; o < output_len;
+       o += gstride) {
     long long ib, ob;
     decode_output(rd, o, &ib, &ob);
     const T* x = in + ib;
@@ -134,7 +135,7 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
   }
 }
 
-template <typename Fold, typename T>
+template <typename Fold, typename T, int BS>
 __device__ __forceinline__ void unit_body(void* out, const void* in, const ReduceDims& rd,
                                           long long output_len, Fold f) {
   T* o = static_cast<T*>(out);
@@ -146,11 +147,11 @@ __device__ __forceinline__ void unit_body(void* out, const void* in, const Reduc
 #pragma unroll
     for (int k = 0; k < kMaxDims; ++k) vector = vector && (k >= rd.n || rd.is[k] % V == 0);
     if (vector) {
-      unit_outputs<Fold, T, true>(o, x, rd, output_len, f);
+      unit_outputs<Fold, T, true, BS>(o, x, rd, output_len, f);
       return;
     }
   }
-  unit_outputs<Fold, T, false>(o, x, rd, output_len, f);
+  unit_outputs<Fold, T, false, BS>(o, x, rd, output_len, f);
 }
 
 // ---- t4a_cuda_reduce: PLANE --------------------------------------------------------
@@ -318,7 +319,7 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
   const T* in = static_cast<const T*>(in_ptr);
   const ReduceDims& rd = pp.dims;
   const int lane = threadIdx.x % W;
-  const long long plane = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / W;
+  const long long plane = (static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x) / W;
   const long long cubes = output_len * splits;
   long long cube = plane * per_plane;
   const long long stop = cube + per_plane < cubes ? cube + per_plane : cubes;
@@ -402,6 +403,95 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
   }
 }
 
+// LEAN plane mapping for a contiguous axis whose every chunk (the longer last
+// one included) holds at most K * 32 groups, so each lane's whole share is the
+// walk's first batch: one cube per 32-lane plane, consecutive planes on
+// consecutive cubes (consecutive memory on an inner axis), all K 16-byte groups
+// of a lane loaded at once, non-temporally. Few registers keep eight
+// wavefronts per SIMD in flight, which is what feeds HBM on this part; the
+// fold is the grouped walk's first batch -- the first group seeds, the others
+// join one at a time -- then the tail element and the xor tree. A float Max /
+// Min first folds in any order with the IEEE maximum / minimum and takes the
+// exact order only when the plane's result is a NaN.
+template <typename Fold, typename T, int K>
+__device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in_ptr,
+                                              const LeanPlan& lp, long long cubes, Fold f) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int W = kWarp;
+  // The block size is the launcher's constant kBlock: reading blockDim would
+  // cost every wavefront a memory round trip (it is an implicit kernel argument
+  // fetched by a vector load) before its first data load is issued.
+  constexpr int kPlanes = kBlock / W;
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const int lane = threadIdx.x % W;
+  const long long planes = static_cast<long long>(gridDim.x) * kPlanes;
+  for (long long cube = static_cast<long long>(blockIdx.x) * kPlanes + threadIdx.x / W;
+       cube < cubes; cube += planes) {
+    // cube = o * splits + split; o over the fused dims, first dim fastest.
+    const unsigned int c32 = static_cast<unsigned int>(cube);
+    unsigned int o = div_by(c32, lp.splits);
+    const unsigned int split = c32 - o * lp.splits.d;
+    long long ib = lp.in_offset;
+    long long pb = lp.out_offset;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      if (k < lp.n) {
+        unsigned int c = o;
+        if (k + 1 < lp.n) {
+          const unsigned int q = div_by(o, lp.ext[k]);
+          c = o - q * lp.ext[k].d;
+          o = q;
+        }
+        ib += static_cast<long long>(c) * lp.is[k];
+        pb += static_cast<long long>(c) * lp.os[k];
+      }
+    }
+    const T* chunk = in + ib + static_cast<long long>(split) * lp.chunk_len;
+    const int len = split + 1 == lp.splits.d ? lp.last_len : static_cast<int>(lp.chunk_len);
+    const int groups = len / V;
+    const int tail = groups * V;
+    Group<T, V> b[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (k == 0 || lane + k * W < groups) {
+        const Vec<T, V> x = nt_load<T, V>(chunk + (lane + k * W) * V);
+        __builtin_memcpy(&b[k], &x, sizeof(b[k]));
+      }
+    }
+    const bool has_tail = lane < len - tail;
+    const T t = has_tail ? chunk[tail + lane] : b[0].x[0];
+    auto exact = [&]() {
+      T acc = group_value<Fold, T, V>(b[0], f);
+#pragma unroll
+      for (int k = 1; k < K; ++k) {
+        if (lane + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(b[k], f));
+      }
+      if (has_tail) acc = f.fold(acc, t);
+      return plane_tree(acc, W, f);
+    };
+    T reduced;
+    using Fast = typename AnyOrder<Fold, T>::type;
+    if constexpr (!std::is_void_v<Fast>) {
+      // Without a NaN any order gives the exact result; the tail element and
+      // unloaded groups repeat b[0].x[0], which an extremum ignores.
+      const Fast g;
+      T acc = t;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const bool in_range = k == 0 || lane + k * W < groups;
+#pragma unroll
+        for (int c = 0; c < V; ++c) acc = g.combine(acc, in_range ? b[k].x[c] : b[0].x[0]);
+      }
+      reduced = plane_tree(acc, W, g);
+      if (reduced != reduced) reduced = exact();
+    } else {
+      reduced = exact();
+    }
+    if (lane == 0) partials[pb + static_cast<long long>(split) * lp.out_axis_stride] = reduced;
+  }
+}
+
 // PLANE mapping: plane = W lanes (W = blockDim.x when blockDim.x <= 32, else 32
 // with blockDim.x / 32 planes per block, reference reduce.cu:557-581); planes
 // stride over the cubes.
@@ -475,8 +565,8 @@ __device__ __forceinline__ void partials_columns(void* partials_ptr, const void*
   const ReduceDims& rd = pp.dims;
   const long long stride = rd.axis_stride;
   const int t = threadIdx.x % kWave;
-  const long long nwaves = static_cast<long long>(gridDim.x) * blockDim.x / kWave;
-  for (long long u = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = static_cast<long long>(gridDim.x) * (kBlock / kWave);
+  for (long long u = (static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
        u < pp.units; u += nwaves) {
     const long long col = (u % pp.col_blocks) * kWave + t;
     if (col >= pp.columns) continue;
@@ -521,8 +611,8 @@ __device__ __forceinline__ void partials_rows(void* partials_ptr, const void* in
   const int t = threadIdx.x % kWave;
   const int c = t % C;
   const int ro = t / C;
-  const long long nwaves = static_cast<long long>(gridDim.x) * blockDim.x / kWave;
-  for (long long u = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const long long nwaves = static_cast<long long>(gridDim.x) * (kBlock / kWave);
+  for (long long u = (static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
        u < pp.units; u += nwaves) {
     long long ib, pb, split;
     decode_unit(pp, u, c, &ib, &pb, &split, splits);
@@ -661,7 +751,7 @@ __device__ __forceinline__ void reduce_run(void* out, const void* in, int op, bo
     if (plane) {
       plane_body<decltype(fold), T>(out, in, rd, output_len, fold, warp_lds);
     } else {
-      unit_body<decltype(fold), T>(out, in, rd, output_len, fold);
+      unit_body<decltype(fold), T, 0>(out, in, rd, output_len, fold);
     }
   });
 }
@@ -675,6 +765,15 @@ __global__ void __launch_bounds__(512)
                   long long output_len) {
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(T)];
   reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds);
+}
+
+// UNIT with the planner's kBlock-thread blocks.
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+    reduce_unit_kernel(void* out, const void* in, int op, ReduceDims rd, long long output_len) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    unit_body<decltype(fold), T, kBlock>(out, in, rd, output_len, fold);
+  });
 }
 
 template <typename T>
@@ -696,6 +795,17 @@ __global__ void __launch_bounds__(256)
       if constexpr (decltype(fold)::kRegroup)
         partials_stream<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
                                            per_plane, fold);
+    });
+  }
+}
+
+template <typename T, int K>
+__global__ void __launch_bounds__(kBlock)
+    partials_lean_kernel(void* partials, const void* in, int op, LeanPlan lp, long long cubes) {
+  if constexpr (VecLanes<T>::value > 0) {
+    dispatch_fold<T>(op, [&](auto fold) {
+      if constexpr (decltype(fold)::kRegroup)
+        partials_lean<decltype(fold), T, K>(partials, in, lp, cubes, fold);
     });
   }
 }
@@ -792,8 +902,15 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   return with_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
-    hipLaunchKernelGGL(t4a::reduce_kernel<T>, grid, block, 0, static_cast<hipStream_t>(stream),
-                       out, in, op, strategy, rd, output_len);
+    const unsigned threads = block.x * block.y * block.z;
+    if (strategy == T4A_CUDA_REDUCE_UNIT && threads == static_cast<unsigned>(t4a::kBlock)) {
+      hipLaunchKernelGGL(t4a::reduce_unit_kernel<T>, grid, block, 0,
+                         static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
+    } else {
+      hipLaunchKernelGGL(t4a::reduce_kernel<T>, grid, block, 0,
+                         static_cast<hipStream_t>(stream), out, in, op, strategy, rd,
+                         output_len);
+    }
     return status_of_last_launch();
   });
 }
@@ -810,18 +927,21 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
   if (partials == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   const unsigned threads = launch->block[0] * launch->block[1] * launch->block[2];
   const int w = threads <= 32u ? static_cast<int>(threads) : t4a::kWarp;
-  const bool whole_waves = launch->block[1] == 1 && launch->block[2] == 1 && threads >= 64u &&
-                           threads % 64u == 0;
+  // The wavefront-wide mappings run in the planner's kBlock-thread blocks.
+  const bool whole_waves = launch->block[1] == 1 && launch->block[2] == 1 &&
+                           threads == static_cast<unsigned>(t4a::kBlock);
   t4a::PartialsPlan pp;
   t4a::partials_plan(&pp, *partials_layout, *in_layout, axis, output_len, splits, w,
                      whole_waves && t4a::sideways_dtype(dtype));
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   const bool sideways = pp.mode != t4a::kPartialsPlane;
-  const bool stream_mode =
-      !sideways && whole_waves &&
-      t4a::stream_applies(pp, dtype, op, chunk_len, w) &&
-      (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  const bool aligned_in = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  const int lean = !sideways && whole_waves && aligned_in
+                       ? t4a::lean_slots(pp, dtype, op, splits, chunk_len, w)
+                       : 0;
+  const bool stream_mode = !lean && !sideways && whole_waves && aligned_in &&
+                           t4a::stream_applies(pp, dtype, op, chunk_len, w);
   // Streaming planes split the cubes evenly over the launched planes (whole
   // wavefronts, so at least two planes per block).
   long long per_plane = 1;
@@ -831,7 +951,29 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
   }
   return with_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
-    if (stream_mode) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (lean > 0) {
+      const t4a::LeanPlan lp = t4a::lean_plan(pp, splits, chunk_len);
+      const long long cubes = output_len * splits;
+      switch (lean) {
+        case 1:
+          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 1>), grid, block, 0, s, partials, in,
+                             op, lp, cubes);
+          break;
+        case 2:
+          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 2>), grid, block, 0, s, partials, in,
+                             op, lp, cubes);
+          break;
+        case 3:
+          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 3>), grid, block, 0, s, partials, in,
+                             op, lp, cubes);
+          break;
+        default:
+          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 4>), grid, block, 0, s, partials, in,
+                             op, lp, cubes);
+          break;
+      }
+    } else if (stream_mode) {
       hipLaunchKernelGGL(t4a::partials_stream_kernel<T>, grid, block, 0,
                          static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
                          splits, chunk_len, per_plane);

@@ -222,6 +222,59 @@ def test_special_values():
             run(dtype, op, t.Layout.compact(ext), 0, t.Layout.compact([1, 3]), 32, data)
 
 
+def test_extrema_nan_payloads_bit_exact():
+    """Max / Min select an operand, so their results are exact bytes even for NaN
+    payloads: several payloads (quiet, signalling, negative) in one chunk, in
+    the tail, rows of signed zeros only, infinities -- on the contiguous-axis
+    pass 1 whose any-order fast fold hands NaN results to the exact order."""
+    rng = np.random.default_rng(11)
+    rows, n = 24, 8192
+    payloads = {F32: [0x7FC00001, 0x7F800001, 0xFFC00123, 0x7FFFFFFF, 0xFF800002],
+                F64: [0x7FF8000000000001, 0x7FF0000000000001, 0xFFF8000000000123,
+                      0x7FFFFFFFFFFFFFFF, 0xFFF0000000000002]}
+    for dtype in (F32, F64):
+        bits = np.uint32 if dtype == F32 else np.uint64
+        for op in (Max, Min):
+            data = values(dtype, op, rows * n, rng)
+            raw = data.view(bits)
+            pl = payloads[dtype]
+            raw[3] = pl[0]                                  # row 0, chunk 0
+            raw[n + 10], raw[n + 200], raw[n + 201] = pl[1], pl[2], pl[0]  # row 1, one chunk
+            raw[2 * n + 255] = pl[3]                        # last element of a chunk
+            raw[3 * n + n - 1] = pl[4]                      # last element of the row
+            raw[4 * n + 7], raw[4 * n + 4000] = pl[2], pl[1]  # two chunks of one row
+            data[5 * n:6 * n] = -0.0                        # signed zeros only
+            data[5 * n + 1234] = 0.0
+            data[6 * n:7 * n] = 0.0
+            data[6 * n + 99] = -0.0
+            data[7 * n + 50] = np.inf
+            data[8 * n + 60] = -np.inf
+            in_l = t.Layout.compact([n, rows])
+            out_l = t.Layout.compact([1, rows])
+            plan = t.plan_reduction(dtype, op, out_l, rows, in_l, rows * n, 0, 32)
+            assert plan.kind == "Split" and plan.split.chunk_len == 256
+            say("extrema payloads", dtype.name, op.name)
+            pl_l = t.reduction_partials_layout(in_l, 0, plan.split.splits)
+            pn = pl_l.element_count()
+            d_in, d_out, d_part = to_device(data), sentinel(rows * dtype.size), sentinel(
+                pn * dtype.size)
+            hip.enqueue_reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, 0, rows,
+                                  stream())
+            want_part = np.zeros(pn, dtype=NUMPY[dtype])
+            orc.reduce_partials(want_part, data, dtype, op, 32, pl_l, in_l, 0, rows,
+                                plan.split.splits, plan.split.chunk_len)
+            want = np.zeros(rows, dtype=NUMPY[dtype])
+            orc.reduce(want, want_part, dtype, plan.combine_op, plan.combine_strategy, 32, out_l,
+                       pl_l, 0, rows)
+            got_part = to_host(d_part, pn * dtype.size, "partials")
+            got = to_host(d_out, rows * dtype.size, "output")
+            assert np.array_equal(got_part, want_part.view(np.uint8)), (dtype, op, "partials")
+            assert np.array_equal(got, want.view(np.uint8)), (dtype, op, "finals")
+            assert np.isnan(want[:5]).all() and not np.isnan(want[5:]).any()
+            zero_sign = np.signbit(want[5:7])
+            assert list(zero_sign) == ([False, False] if op == Max else [True, True])
+
+
 def test_empty_output_is_no_launch():
     in_l = t.Layout.compact([5, 0])
     out_l = t.Layout.compact([1, 0])
