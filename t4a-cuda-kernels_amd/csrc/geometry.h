@@ -348,56 +348,89 @@ T4A_HD bool sideways_dtype(int dtype) {
          dtype == T4A_CUDA_I64;
 }
 
-// Pass-1 work mapping (t4a_cuda_reduce_partials). All three keep the
-// reference's per-plane topology; they differ only in which hardware lanes hold
-// which plane lanes:
+// Pass-1 work mapping (t4a_cuda_reduce_partials). All of them keep the
+// reference's per-plane topology -- plane lane l folds rows start + l + 32k in k
+// order, then the own-left xor tree -- and differ only in which hardware lanes
+// hold which plane lanes:
 //   PLANE      one 32-lane half-wavefront per (output, split) cube, as the
 //              reference warp (any width 8/16/32);
-//   COLUMNS    a strided axis whose fastest non-axis dim (input stride 1) has
-//              at least 64 columns: one lane per column, holding all 32 plane
-//              lanes of that column's cube in registers, so every load of the
-//              wavefront reads 64 adjacent columns of one row;
-//   ROWS       the same with 2..32 columns (a power of two): 64 / C rows per
-//              load, each lane holding the 32 / (64 / C) plane lanes of its
-//              row residue.
-// COLUMNS and ROWS need 32-lane planes and blocks made of whole wavefronts.
-enum PartialsMode { kPartialsPlane = 0, kPartialsColumns = 1, kPartialsRows = 2 };
+//   TILES      a strided axis whose fastest non-axis dim (input stride 1) has
+//              at least 64 columns: a block of four wavefronts per (column
+//              block, split); lane t holds `cpl` adjacent columns (one 8-byte
+//              load for two 4-byte columns) and wavefront w the plane lanes
+//              8w..8w+7 of those columns' cubes; the four wavefronts' subtrees
+//              meet through LDS;
+//   VECROWS    rows of c = 2 or 4 contiguous elements (8 or 16 bytes): a 32-lane
+//              plane per (split, other) takes all c columns, each plane lane
+//              loading whole rows, one xor tree per column;
+//   ROWS       2..32 columns (a power of two) otherwise: 64 / C rows per
+//              wavefront load, each lane holding the 32 / (64 / C) plane lanes of
+//              its row residue.
+// The wavefront mappings need 32-lane planes and kBlock-thread blocks.
+enum PartialsMode {
+  kPartialsPlane = 0,
+  kPartialsRows = 2,
+  kPartialsTiles = 3,
+  kPartialsVecRows = 4
+};
 
 struct PartialsPlan {
   int mode;
   ReduceDims dims;
-  int col_dim;          // fused dim of input stride 1 (COLUMNS/ROWS)
+  int col_dim;          // fused dim of input stride 1 (TILES/VECROWS/ROWS)
+  int cpl;              // columns per lane: TILES 1 or 2, VECROWS c
   long long columns;    // its extent
-  long long col_blocks; // 64-column blocks (COLUMNS), 1 (ROWS)
+  long long col_os;     // partials stride of that dim
+  long long col_blocks; // column blocks of 64 * cpl (TILES), else 1
   long long others;     // product of the other fused extents
-  long long units;      // wavefront work items (COLUMNS/ROWS) or cubes (PLANE)
+  long long units;      // blocks (TILES), planes (VECROWS), wavefronts (ROWS), cubes
 };
 
+// `align`: the input pointer's alignment in bytes (the planner, which has no
+// pointer, assumes 16; the launcher passes the real one). A plan made for a
+// better-aligned pointer still runs correctly through the launcher, which
+// re-plans, because every mapping walks its units grid-stride.
 T4A_HD void partials_plan(PartialsPlan* p, const t4a_cuda_layout& partials,
                           const t4a_cuda_layout& in, int axis, long long output_len,
-                          long long splits, int plane_width, int whole_waves) {
+                          long long splits, int plane_width, int whole_waves, int esize,
+                          int align) {
   reduce_dims(&p->dims, partials, in, axis);
+  const ReduceDims& d = p->dims;
   p->mode = kPartialsPlane;
   p->col_dim = -1;
+  p->cpl = 1;
   p->columns = 0;
+  p->col_os = 0;
   p->col_blocks = 0;
   p->others = 0;
   p->units = output_len * splits;
-  if (plane_width != kWarp || !whole_waves || p->dims.axis_stride == 1 || output_len <= 0)
-    return;
+  if (plane_width != kWarp || !whole_waves || d.axis_stride == 1 || output_len <= 0) return;
   int col = -1;
-  for (int k = 0; k < p->dims.n; ++k) {
-    if (p->dims.is[k] == 1) col = k;
+  for (int k = 0; k < d.n; ++k) {
+    if (d.is[k] == 1) col = k;
   }
   if (col < 0) return;
-  const long long c = p->dims.ext[col];
+  const long long c = d.ext[col];
   long long others = 1;
-  for (int k = 0; k < p->dims.n; ++k) {
-    if (k != col) others *= p->dims.ext[k];
+  for (int k = 0; k < d.n; ++k) {
+    if (k != col) others *= d.ext[k];
   }
+  // Every row start of the column dim a multiple of v elements from the base.
+  auto rows_multiple_of = [&](long long v) {
+    if (d.in_offset % v != 0 || d.axis_stride % v != 0) return false;
+    for (int k = 0; k < d.n; ++k) {
+      if (k != col && d.is[k] % v != 0) return false;
+    }
+    return true;
+  };
   if (c >= kWave) {
-    p->mode = kPartialsColumns;
-    p->col_blocks = (c + kWave - 1) / kWave;
+    p->mode = kPartialsTiles;
+    p->cpl = esize == 4 && align >= 8 && c % 2 == 0 && rows_multiple_of(2) ? 2 : 1;
+    p->col_blocks = (c + kWave * p->cpl - 1) / (kWave * p->cpl);
+  } else if ((c * esize == 8 || c * esize == 16) && align >= c * esize && rows_multiple_of(c)) {
+    p->mode = kPartialsVecRows;
+    p->cpl = static_cast<int>(c);
+    p->col_blocks = 1;
   } else if (c >= 2 && (c & (c - 1)) == 0) {
     p->mode = kPartialsRows;
     p->col_blocks = 1;
@@ -406,8 +439,15 @@ T4A_HD void partials_plan(PartialsPlan* p, const t4a_cuda_layout& partials,
   }
   p->col_dim = col;
   p->columns = c;
+  p->col_os = d.os[col];
   p->others = others;
   p->units = p->col_blocks * others * splits;
+  // TILES and VECROWS walk a SidePlan: at most two other dims, 32-bit counts.
+  if ((p->mode == kPartialsTiles || p->mode == kPartialsVecRows) &&
+      (d.n > 3 || d.axis_len >= (1ll << 31) || p->units >= (1ll << 31))) {
+    p->mode = kPartialsPlane;
+    p->units = output_len * splits;
+  }
 }
 
 // Whether pass 1 can stream whole runs of cubes through the grouped walk: a
@@ -476,6 +516,57 @@ T4A_HD LeanPlan lean_plan(const PartialsPlan& p, long long splits, long long chu
   lp.chunk_len = chunk_len;
   lp.out_axis_stride = rd.out_axis_stride;
   return lp;
+}
+
+// The TILES / VECROWS mappings' own plan: unit u = (column block, split,
+// other) decoded with precomputed divisors over at most two other fused dims,
+// the rest as element offsets and strides.
+struct SidePlan {
+  long long in_offset;
+  long long out_offset;
+  long long axis_stride;      // input elements between rows
+  long long out_axis_stride;  // partials elements between splits
+  long long col_os;           // partials elements between columns
+  long long is[2];
+  long long os[2];
+  FastDiv ext[2];
+  FastDiv col_blocks;
+  FastDiv splits;
+  int n_other;
+  int chunk_len;
+  int last_len;
+  long long columns;
+  long long units;
+};
+
+T4A_HD SidePlan side_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
+  SidePlan sp;
+  const ReduceDims& d = p.dims;
+  sp.in_offset = d.in_offset;
+  sp.out_offset = d.out_offset;
+  sp.axis_stride = d.axis_stride;
+  sp.out_axis_stride = d.out_axis_stride;
+  sp.col_os = p.col_os;
+  sp.n_other = 0;
+  for (int k = 0; k < 2; ++k) {
+    sp.is[k] = 0;
+    sp.os[k] = 0;
+    sp.ext[k] = fast_div(1);
+  }
+  for (int k = 0; k < d.n; ++k) {
+    if (k == p.col_dim || sp.n_other == 2) continue;
+    sp.is[sp.n_other] = d.is[k];
+    sp.os[sp.n_other] = d.os[k];
+    sp.ext[sp.n_other] = fast_div(static_cast<unsigned int>(d.ext[k]));
+    ++sp.n_other;
+  }
+  sp.col_blocks = fast_div(static_cast<unsigned int>(p.col_blocks));
+  sp.splits = fast_div(static_cast<unsigned int>(splits));
+  sp.chunk_len = static_cast<int>(chunk_len);
+  sp.last_len = static_cast<int>(d.axis_len - (splits - 1) * chunk_len);
+  sp.columns = p.columns;
+  sp.units = p.units;
+  return sp;
 }
 
 // Cubes each streaming plane takes: enough planes to fill the chip (16384, four

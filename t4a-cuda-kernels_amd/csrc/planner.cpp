@@ -501,9 +501,13 @@ int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_
   }
   t4a::PartialsPlan plan;
   t4a::partials_plan(&plan, *partials_layout, *in_layout, static_cast<int>(axis), output_len,
-                     split.splits, t4a::kWarp, t4a::sideways_dtype(dtype));
-  long long per_block =
-      plan.mode == t4a::kPartialsPlane ? kBlock / t4a::kWarp : kBlock / t4a::kWave;
+                     split.splits, t4a::kWarp, t4a::sideways_dtype(dtype), es, 16);
+  // Units per block: one (TILES), a plane per 32 lanes (PLANE, VECROWS), a
+  // wavefront per 64 (ROWS).
+  long long per_block = kBlock / t4a::kWave;
+  if (plan.mode == t4a::kPartialsTiles) per_block = 1;
+  if (plan.mode == t4a::kPartialsPlane || plan.mode == t4a::kPartialsVecRows)
+    per_block = kBlock / t4a::kWarp;
   // Lean planes take one cube each; streaming planes take runs of cubes.
   if (!t4a::lean_slots(plan, dtype, op, split.splits, split.chunk_len, t4a::kWarp) &&
       t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))

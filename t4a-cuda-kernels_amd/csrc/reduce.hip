@@ -553,44 +553,201 @@ __device__ __forceinline__ void decode_unit(const PartialsPlan& pp, long long u,
   *pb = p_base;
 }
 
-// COLUMNS: wavefront lane t holds column cb*64 + t and all 32 plane lanes of its
-// cube: plane lane l folds rows start + l + 32k in k order; the register tree is
-// the plane's xor tree.
-template <typename Fold, typename T>
-__device__ __forceinline__ void partials_columns(void* partials_ptr, const void* in_ptr,
-                                                 const PartialsPlan& pp, long long chunk_len,
-                                                 long long splits, Fold f) {
+// Load `N` adjacent elements (N = 1, 2 or 4; aligned to N elements) as one
+// non-temporal access.
+template <typename T, int N>
+__device__ __forceinline__ Vec<T, N> load_n(const T* p) {
+  return nt_load<T, N>(p);
+}
+
+// One plane lane's serial walk over rows q0, q0 + 32, ... below `len` of its
+// chunk (q0 < len), each row N adjacent elements, folded in that order into
+// `acc` (seeded from row q0); eight loads are issued per step. Row q0 of this
+// lane sits at `base + lane_off` bytes and row q0 + 32k `k * step` bytes on;
+// where the caller makes `base` and `step` the same for the whole wavefront,
+// every load takes the scalar-base addressing form.
+template <int N, typename Fold, typename T>
+__device__ __forceinline__ void fold_lane_rows(const char* base, long long step,
+                                               long long lane_off, int q0, int len, Fold f,
+                                               T* acc) {
+  constexpr int kStep = 8;
+  auto at = [&](int k) {
+    return reinterpret_cast<const T*>(base + k * step + lane_off);
+  };
+  Vec<T, N> v[kStep];
+#pragma unroll
+  for (int k = 0; k < kStep; ++k) {
+    if (k == 0 || q0 + k * kWarp < len) v[k] = load_n<T, N>(at(k));
+  }
+#pragma unroll
+  for (int c = 0; c < N; ++c) acc[c] = f.seed(v[0].v[c]);
+#pragma unroll
+  for (int k = 1; k < kStep; ++k) {
+    if (q0 + k * kWarp < len) {
+#pragma unroll
+      for (int c = 0; c < N; ++c) acc[c] = f.fold(acc[c], v[k].v[c]);
+    }
+  }
+  for (int b = kStep; q0 + b * kWarp < len; b += kStep) {
+#pragma unroll
+    for (int k = 0; k < kStep; ++k) {
+      if (q0 + (b + k) * kWarp < len) v[k] = load_n<T, N>(at(b + k));
+    }
+#pragma unroll
+    for (int k = 0; k < kStep; ++k) {
+      if (q0 + (b + k) * kWarp < len) {
+#pragma unroll
+        for (int c = 0; c < N; ++c) acc[c] = f.fold(acc[c], v[k].v[c]);
+      }
+    }
+  }
+}
+
+// Unit u = (column block, split, other) of a SidePlan: input element offset of
+// the block's first column at the split's first row, partials offset of that
+// column's partial, and the split's length.
+__device__ __forceinline__ void side_unit(const SidePlan& sp, unsigned int u,
+                                          unsigned int* block, long long* ib, long long* pb,
+                                          int* len) {
+  const unsigned int rest = div_by(u, sp.col_blocks);
+  *block = u - rest * sp.col_blocks.d;
+  unsigned int other = div_by(rest, sp.splits);
+  const unsigned int split = rest - other * sp.splits.d;
+  long long in_base = sp.in_offset + static_cast<long long>(split) * sp.chunk_len * sp.axis_stride;
+  long long p_base = sp.out_offset + static_cast<long long>(split) * sp.out_axis_stride;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (k < sp.n_other) {
+      unsigned int c = other;
+      if (k + 1 < sp.n_other) {
+        const unsigned int q = div_by(other, sp.ext[k]);
+        c = other - q * sp.ext[k].d;
+        other = q;
+      }
+      in_base += static_cast<long long>(c) * sp.is[k];
+      p_base += static_cast<long long>(c) * sp.os[k];
+    }
+  }
+  *ib = in_base;
+  *pb = p_base;
+  *len = split + 1 == sp.splits.d ? sp.last_len : sp.chunk_len;
+}
+
+// TILES: a block of four wavefronts per unit (column block, split, other).
+// Lane t holds columns col0 .. col0 + CPL - 1 and wavefront w the plane lanes
+// l = 8w .. 8w + 7 of those columns' cubes; plane lane l folds rows
+// start + l + 32k in k order. A wavefront joins its eight plane lanes with the
+// pairwise tree as they finish (a binary counter over l), and the four subtree
+// values meet through LDS as ((w0 + w1) + (w2 + w3)): together, the plane's
+// own-left xor tree.
+template <typename Fold, typename T, int CPL>
+__device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* in_ptr,
+                                               const SidePlan& sp, Fold f, T* lds) {
+  constexpr int kWaves = kBlock / kWave;
+  constexpr int kLanesPerWave = kWarp / kWaves;  // plane lanes per wavefront: 8
+  constexpr int BC = kWave * CPL;                // columns per block
+  static_assert(kLanesPerWave == 8, "the streaming tree below is written for 8 lanes");
   T* partials = static_cast<T*>(partials_ptr);
-  const T* in = static_cast<const T*>(in_ptr);
-  const ReduceDims& rd = pp.dims;
-  const long long stride = rd.axis_stride;
+  const char* in = static_cast<const char*>(in_ptr);
+  // The wavefront index, explicitly uniform: the compiler cannot tell that
+  // threadIdx.x / 64 is, and would otherwise turn every row test below into a
+  // divergent branch.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int t = threadIdx.x % kWave;
-  const long long nwaves = static_cast<long long>(gridDim.x) * (kBlock / kWave);
-  for (long long u = (static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
-       u < pp.units; u += nwaves) {
-    const long long col = (u % pp.col_blocks) * kWave + t;
-    if (col >= pp.columns) continue;
-    long long ib, pb, split;
-    decode_unit(pp, u, col, &ib, &pb, &split, splits);
-    const long long start = split * chunk_len;
-    const long long end = split + 1 == splits ? rd.axis_len : start + chunk_len;
-    const T* x = in + ib;
-    T acc[kWarp];
+  const long long row_bytes = sp.axis_stride * static_cast<long long>(sizeof(T));
+  const long long lane_off = static_cast<long long>(t) * CPL * static_cast<long long>(sizeof(T));
+  for (long long u = blockIdx.x; u < sp.units; u += gridDim.x) {
+    unsigned int block;
+    long long ib, pb;
+    int len;
+    side_unit(sp, static_cast<unsigned int>(u), &block, &ib, &pb, &len);
+    const long long block_col = static_cast<long long>(block) * BC;
+    const bool active = block_col + t * CPL < sp.columns;  // CPL divides the column count
+    // the block's first column at row 0 of the split, uniform across the block
+    const char* rows = in + (ib + block_col) * static_cast<long long>(sizeof(T));
+    T level[3][CPL];
+    T sub[CPL];
+    // Two plane lanes per step keep two lanes' loads in flight; the tree's
+    // climb is a uniform branch on the lane index.
+#pragma unroll 2
+    for (int a = 0; a < kLanesPerWave; ++a) {
+      T acc[CPL];
+      const int q0 = w * kLanesPerWave + a;
+      if (active) {
+        fold_lane_rows<CPL>(rows + q0 * row_bytes, kWarp * row_bytes, lane_off, q0, len, f,
+                            acc);
+      } else {
 #pragma unroll
-    for (int l = 0; l < kWarp; ++l) acc[l] = f.seed(x[(start + l) * stride]);
-    long long r0 = start + kWarp;
-    for (; r0 + kWarp <= end; r0 += kWarp) {
-      T v[kWarp];
+        for (int c = 0; c < CPL; ++c) acc[c] = T{};
+      }
+      // Binary counter: lane a's value climbs while a ends in ones.
+      if ((a & 1) == 0) {
 #pragma unroll
-      for (int l = 0; l < kWarp; ++l) v[l] = x[(r0 + l) * stride];
+        for (int c = 0; c < CPL; ++c) level[0][c] = acc[c];
+      } else {
 #pragma unroll
-      for (int l = 0; l < kWarp; ++l) acc[l] = f.fold(acc[l], v[l]);
+        for (int c = 0; c < CPL; ++c) acc[c] = f.combine(level[0][c], acc[c]);
+        if ((a & 2) == 0) {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) level[1][c] = acc[c];
+        } else {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) acc[c] = f.combine(level[1][c], acc[c]);
+          if ((a & 4) == 0) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) level[2][c] = acc[c];
+          } else {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) sub[c] = f.combine(level[2][c], acc[c]);
+          }
+        }
+      }
     }
 #pragma unroll
-    for (int l = 0; l < kWarp; ++l) {
-      if (r0 + l < end) acc[l] = f.fold(acc[l], x[(r0 + l) * stride]);
+    for (int c = 0; c < CPL; ++c) lds[w * BC + t * CPL + c] = sub[c];
+    __syncthreads();
+    if (w == 0 && active) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int i = t * CPL + c;
+        const T r = f.combine(f.combine(lds[i], lds[BC + i]),
+                              f.combine(lds[2 * BC + i], lds[3 * BC + i]));
+        partials[pb + (block_col + i) * sp.col_os] = r;
+      }
     }
-    partials[pb] = register_tree<kWarp>(acc, f);
+    __syncthreads();  // the LDS tile is reused by the block's next unit
+  }
+}
+
+// VECROWS: rows of C contiguous elements (8 or 16 bytes). A 32-lane plane takes
+// unit u = (split, other), i.e. the cubes of all C columns; plane lane l loads
+// whole rows start + l + 32k and folds each column in k order, then one xor tree
+// per column.
+template <typename Fold, typename T, int C>
+__device__ __forceinline__ void partials_vecrows(void* partials_ptr, const void* in_ptr,
+                                                 const SidePlan& sp, Fold f) {
+  constexpr int W = kWarp;
+  constexpr int kPlanes = kBlock / W;
+  T* partials = static_cast<T*>(partials_ptr);
+  const char* in = static_cast<const char*>(in_ptr);
+  const int lane = threadIdx.x % W;
+  const long long row_bytes = sp.axis_stride * static_cast<long long>(sizeof(T));
+  const long long planes = static_cast<long long>(gridDim.x) * kPlanes;
+  for (long long u = static_cast<long long>(blockIdx.x) * kPlanes + threadIdx.x / W;
+       u < sp.units; u += planes) {
+    unsigned int block;
+    long long ib, pb;
+    int len;
+    side_unit(sp, static_cast<unsigned int>(u), &block, &ib, &pb, &len);
+    T acc[C];
+    fold_lane_rows<C>(in + ib * static_cast<long long>(sizeof(T)), kWarp * row_bytes,
+                      lane * row_bytes, lane, len, f, acc);
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = plane_tree(acc[c], W, f);
+    if (lane == 0) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) partials[pb + c * sp.col_os] = acc[c];
+    }
   }
 }
 
@@ -682,29 +839,6 @@ __device__ __forceinline__ void partials_rows(void* partials_ptr, const void* in
     }
     if (ro == 0) partials[pb] = acc[0];
   }
-}
-
-template <typename Fold, typename T>
-__device__ __forceinline__ void partials_body(void* partials, const void* in,
-                                              const PartialsPlan& pp, long long output_len,
-                                              long long splits, long long chunk_len, Fold f) {
-  if constexpr (VecLanes<T>::value > 0) {
-    if (pp.mode == kPartialsColumns) {
-      partials_columns<Fold, T>(partials, in, pp, chunk_len, splits, f);
-      return;
-    }
-    if (pp.mode == kPartialsRows) {
-      switch (pp.columns) {
-        case 2: partials_rows<1, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
-        case 4: partials_rows<2, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
-        case 8: partials_rows<4, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
-        case 16: partials_rows<8, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
-        case 32: partials_rows<16, Fold, T>(partials, in, pp, chunk_len, splits, f); return;
-        default: break;
-      }
-    }
-  }
-  partials_planes<Fold, T>(partials, in, pp, output_len, splits, chunk_len, f);
 }
 
 // Fold dispatch for element type T over the reference's supported pairs
@@ -810,12 +944,29 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256)
-    partials_sideways_kernel(void* partials, const void* in, int op, PartialsPlan pp,
-                             long long output_len, long long splits, long long chunk_len) {
+template <typename T, int CPL>
+__global__ void __launch_bounds__(kBlock)
+    partials_tiles_kernel(void* partials, const void* in, int op, SidePlan sp) {
+  __shared__ T lds[(kBlock / kWave) * kWave * CPL];
   dispatch_fold<T>(op, [&](auto fold) {
-    partials_body<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len, fold);
+    partials_tiles<decltype(fold), T, CPL>(partials, in, sp, fold, lds);
+  });
+}
+
+template <typename T, int C>
+__global__ void __launch_bounds__(kBlock)
+    partials_vecrows_kernel(void* partials, const void* in, int op, SidePlan sp) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    partials_vecrows<decltype(fold), T, C>(partials, in, sp, fold);
+  });
+}
+
+template <typename T, int A>
+__global__ void __launch_bounds__(kBlock)
+    partials_rows_kernel(void* partials, const void* in, int op, PartialsPlan pp,
+                         long long splits, long long chunk_len) {
+  dispatch_fold<T>(op, [&](auto fold) {
+    partials_rows<A, decltype(fold), T>(partials, in, pp, chunk_len, splits, fold);
   });
 }
 
@@ -851,7 +1002,8 @@ extern "C" __global__ void __launch_bounds__(256)
   __shared__ t4a::PartialsPlan pp;
   if (threadIdx.x == 0) {
     const int w = blockDim.x <= 32u ? static_cast<int>(blockDim.x) : t4a::kWarp;
-    t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, w, 0);
+    t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, w, 0,
+                       t4a::dtype_size(dtype), 1);
   }
   __syncthreads();
   t4a::dispatch_dtype(dtype, [&](auto* tag) {
@@ -930,9 +1082,11 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
   // The wavefront-wide mappings run in the planner's kBlock-thread blocks.
   const bool whole_waves = launch->block[1] == 1 && launch->block[2] == 1 &&
                            threads == static_cast<unsigned>(t4a::kBlock);
+  const uintptr_t address = reinterpret_cast<uintptr_t>(in);
+  const int align = (address & 15) == 0 ? 16 : (address & 7) == 0 ? 8 : (address & 3) == 0 ? 4 : 1;
   t4a::PartialsPlan pp;
   t4a::partials_plan(&pp, *partials_layout, *in_layout, axis, output_len, splits, w,
-                     whole_waves && t4a::sideways_dtype(dtype));
+                     whole_waves && t4a::sideways_dtype(dtype), t4a::dtype_size(dtype), align);
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   const bool sideways = pp.mode != t4a::kPartialsPlane;
@@ -978,9 +1132,48 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
                          static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
                          splits, chunk_len, per_plane);
     } else if (sideways) {
-      hipLaunchKernelGGL(t4a::partials_sideways_kernel<T>, grid, block, 0,
-                         static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
-                         splits, chunk_len);
+      if constexpr (t4a::VecLanes<T>::value > 0) {
+        // sideways modes are planned for real and integer types only
+        const t4a::SidePlan sp = t4a::side_plan(pp, splits, chunk_len);
+        if (pp.mode == t4a::kPartialsTiles) {
+          if (pp.cpl == 2)
+            hipLaunchKernelGGL((t4a::partials_tiles_kernel<T, 2>), grid, block, 0, s, partials,
+                               in, op, sp);
+          else
+            hipLaunchKernelGGL((t4a::partials_tiles_kernel<T, 1>), grid, block, 0, s, partials,
+                               in, op, sp);
+        } else if (pp.mode == t4a::kPartialsVecRows) {
+          if (pp.cpl == 4)
+            hipLaunchKernelGGL((t4a::partials_vecrows_kernel<T, 4>), grid, block, 0, s,
+                               partials, in, op, sp);
+          else
+            hipLaunchKernelGGL((t4a::partials_vecrows_kernel<T, 2>), grid, block, 0, s,
+                               partials, in, op, sp);
+        } else {
+          switch (pp.columns) {
+            case 2:
+              hipLaunchKernelGGL((t4a::partials_rows_kernel<T, 1>), grid, block, 0, s, partials,
+                                 in, op, pp, splits, chunk_len);
+              break;
+            case 4:
+              hipLaunchKernelGGL((t4a::partials_rows_kernel<T, 2>), grid, block, 0, s, partials,
+                                 in, op, pp, splits, chunk_len);
+              break;
+            case 8:
+              hipLaunchKernelGGL((t4a::partials_rows_kernel<T, 4>), grid, block, 0, s, partials,
+                                 in, op, pp, splits, chunk_len);
+              break;
+            case 16:
+              hipLaunchKernelGGL((t4a::partials_rows_kernel<T, 8>), grid, block, 0, s, partials,
+                                 in, op, pp, splits, chunk_len);
+              break;
+            default:
+              hipLaunchKernelGGL((t4a::partials_rows_kernel<T, 16>), grid, block, 0, s,
+                                 partials, in, op, pp, splits, chunk_len);
+              break;
+          }
+        }
+      }
     } else {
       hipLaunchKernelGGL(t4a::partials_plane_kernel<T>, grid, block, 0,
                          static_cast<hipStream_t>(stream), partials, in, op, pp, output_len,
