@@ -43,7 +43,12 @@ struct TransposeShape {
   static constexpr int TN = sizeof(P) >= 8 ? 64 : 128;
 };
 
-template <typename P, int VL, int VS>
+// BS: the launcher's compile-time block size (0: read blockDim, for the
+// geometry-agnostic entry). With BS known, a whole tile takes the unrolled path:
+// each thread issues all of its loads before the first LDS write and all of its
+// LDS reads before the first store, with no edge tests; edge tiles and the
+// entry take the general loops.
+template <typename P, int VL, int VS, int BS>
 __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __restrict__ src,
                                                 long long src_offset, long long S, long long M,
                                                 long long N, unsigned char* lds) {
@@ -59,9 +64,9 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
   P* d = dst + b * S;
   // Threads and blocks are numbered flat over x and y, so the reference's 2-D
   // geometry (grid (tiles of M, tiles of N, batches), block (tile / vw, rows))
-  // and this build's 1-D persistent one both cover every tile exactly once.
-  const int tid = threadIdx.x + threadIdx.y * blockDim.x;
-  const int nthreads = blockDim.x * blockDim.y;
+  // and this build's 1-D one both cover every tile exactly once.
+  const int tid = threadIdx.x + threadIdx.y * (BS > 0 ? BS : blockDim.x);
+  const int nthreads = BS > 0 ? BS : blockDim.x * blockDim.y;
   const long long nblocks = static_cast<long long>(gridDim.x) * gridDim.y;
   for (long long t = blockIdx.x + static_cast<long long>(blockIdx.y) * gridDim.x;
        t < per_batch; t += nblocks) {
@@ -71,6 +76,51 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
     const long long j0 = tn * TN;
     const int rows = static_cast<int>(M - i0 < TM ? M - i0 : TM);
     const int cols = static_cast<int>(N - j0 < TN ? N - j0 : TN);
+    constexpr int kLoads = BS > 0 ? TM * (TN / VL) / BS : 0;
+    constexpr int kStores = BS > 0 ? TN * (TM / VS) / BS : 0;
+    // The unrolled path holds a thread's whole share in registers: only for
+    // vector accesses (at most eight of them per side).
+    if constexpr (BS > 0 && kLoads <= 8 && kStores <= 8) {
+      static_assert(kLoads * BS == TM * (TN / VL) && kStores * BS == TN * (TM / VS),
+                    "the block divides the tile");
+      if (rows == TM && cols == TN) {
+        Vec<P, VL> x[kLoads];
+#pragma unroll
+        for (int r = 0; r < kLoads; ++r) {
+          const int e = tid + r * BS;
+          const int i = e / (TN / VL);
+          const int j = (e % (TN / VL)) * VL;
+          x[r] = nt_load<P, VL>(s + (i0 + i) * N + j0 + j);
+        }
+#pragma unroll
+        for (int r = 0; r < kLoads; ++r) {
+          const int e = tid + r * BS;
+          const int i = e / (TN / VL);
+          const int j = (e % (TN / VL)) * VL;
+#pragma unroll
+          for (int k = 0; k < VL; ++k) tile[i * PITCH + j + k] = x[r].v[k];
+        }
+        __syncthreads();
+        Vec<P, VS> y[kStores];
+#pragma unroll
+        for (int r = 0; r < kStores; ++r) {
+          const int e = tid + r * BS;
+          const int j = e / (TM / VS);
+          const int i = (e % (TM / VS)) * VS;
+#pragma unroll
+          for (int k = 0; k < VS; ++k) y[r].v[k] = tile[(i + k) * PITCH + j];
+        }
+#pragma unroll
+        for (int r = 0; r < kStores; ++r) {
+          const int e = tid + r * BS;
+          const int j = e / (TM / VS);
+          const int i = (e % (TM / VS)) * VS;
+          nt_store<P, VS>(d + (j0 + j) * M + i0 + i, y[r]);
+        }
+        __syncthreads();
+        continue;
+      }
+    }
     // Source rows: runs of TN along j. VL divides N and src_offset, so a vector
     // is wholly inside or wholly past the matrix edge.
     for (int e = tid; e < TM * (TN / VL); e += nthreads) {
@@ -98,7 +148,7 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
   }
 }
 
-template <typename P>
+template <typename P, int BS>
 __device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
                                                    long long src_offset, long long S,
                                                    long long M, long long N,
@@ -110,13 +160,13 @@ __device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
   if (vl && vs) {
-    transpose_tiles<P, V, V>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, V, V, BS>(d, s, src_offset, S, M, N, lds);
   } else if (vl) {
-    transpose_tiles<P, V, 1>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, V, 1, BS>(d, s, src_offset, S, M, N, lds);
   } else if (vs) {
-    transpose_tiles<P, 1, V>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, 1, V, BS>(d, s, src_offset, S, M, N, lds);
   } else {
-    transpose_tiles<P, 1, 1>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, 1, 1, BS>(d, s, src_offset, S, M, N, lds);
   }
 }
 
@@ -494,13 +544,13 @@ __global__ void __launch_bounds__(256) copy_kernel(void* dst, const void* src, l
   copy_body<P, BS>(dst, src, len);
 }
 
-template <typename P>
+template <typename P, int BS>
 __global__ void __launch_bounds__(512)
     transpose_kernel(void* dst, const void* src, long long src_offset, long long batch_stride,
                      long long dst_fast_extent, long long src_fast_extent) {
   __shared__ alignas(16) unsigned char lds[kTransposeLdsBytes];
-  transpose_dispatch<P>(dst, src, src_offset, batch_stride, dst_fast_extent, src_fast_extent,
-                        lds);
+  transpose_dispatch<P, BS>(dst, src, src_offset, batch_stride, dst_fast_extent,
+                            src_fast_extent, lds);
 }
 
 template <typename P, int VL, int VS>
@@ -534,19 +584,19 @@ extern "C" __global__ void __launch_bounds__(512)
   __shared__ alignas(16) unsigned char lds[t4a::kTransposeLdsBytes];
   switch (t4a::dtype_size(dtype)) {
     case 1:
-      t4a::transpose_dispatch<uint8_t>(dst, src, src_offset, batch_stride, dst_fast_extent,
+      t4a::transpose_dispatch<uint8_t, 0>(dst, src, src_offset, batch_stride, dst_fast_extent,
                                        src_fast_extent, lds);
       break;
     case 4:
-      t4a::transpose_dispatch<uint32_t>(dst, src, src_offset, batch_stride, dst_fast_extent,
+      t4a::transpose_dispatch<uint32_t, 0>(dst, src, src_offset, batch_stride, dst_fast_extent,
                                         src_fast_extent, lds);
       break;
     case 8:
-      t4a::transpose_dispatch<unsigned long long>(dst, src, src_offset, batch_stride,
+      t4a::transpose_dispatch<unsigned long long, 0>(dst, src, src_offset, batch_stride,
                                                   dst_fast_extent, src_fast_extent, lds);
       break;
     case 16:
-      t4a::transpose_dispatch<t4a::Elem16>(dst, src, src_offset, batch_stride, dst_fast_extent,
+      t4a::transpose_dispatch<t4a::Elem16, 0>(dst, src, src_offset, batch_stride, dst_fast_extent,
                                            src_fast_extent, lds);
       break;
     default:
@@ -669,9 +719,13 @@ extern "C" int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype,
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
-    hipLaunchKernelGGL(t4a::transpose_kernel<P>, grid, block, 0,
-                       static_cast<hipStream_t>(stream), dst, src, src_offset, batch_stride,
-                       dst_fast_extent, src_fast_extent);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kTransposeBlock))
+      hipLaunchKernelGGL((t4a::transpose_kernel<P, t4a::kTransposeBlock>), grid, block, 0, s, dst,
+                         src, src_offset, batch_stride, dst_fast_extent, src_fast_extent);
+    else
+      hipLaunchKernelGGL((t4a::transpose_kernel<P, 0>), grid, block, 0, s, dst, src, src_offset,
+                         batch_stride, dst_fast_extent, src_fast_extent);
     return status_of_last_launch();
   });
 }
