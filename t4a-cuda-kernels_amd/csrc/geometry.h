@@ -86,6 +86,10 @@ T4A_HD TransposeTiling transpose_tiling(long long m, long long n, long long batc
 enum MoveMode { kMoveEmpty = 0, kMoveGeneric = 1, kMoveContig = 2, kMoveTiled = 3 };
 
 constexpr int kMaxDims = T4A_CUDA_MAX_RANK;
+// Longest run of a movement tile (entries of each LDS offset table) and the
+// LDS bytes of its padded tile: 64 x 33 16-byte elements, 128 x 33 8-byte ones.
+constexpr long long kMoveRunMax = 128;
+constexpr long long kMoveTileBytes = 64 * 33 * 16;
 
 struct MovePlan {
   int mode;
@@ -183,30 +187,40 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
     return;
   }
   // Tile budget: 4096 elements up to 8 bytes (<= 32 KiB of LDS), 2048 for
-  // 16-byte elements; each run aims for 64 elements.
-  const long long target_a = 64;
-  const long long target_b = esize >= 16 ? 32 : 64;
-  // Grow a run along its chain: each next dim's stride on that side equals the
-  // run's span so far; a dim of the other chain ends it.
+  // 16-byte elements; each run aims for 64 elements (32 for 16-byte elements
+  // on the source side). A run whose chain ends short leaves its share of the
+  // budget to the other run, up to kMoveRunMax elements (a power of two), as
+  // long as the padded tile fits kMoveTileBytes: a 32-element source run
+  // then feeds 128-element destination runs.
+  const long long budget = esize >= 16 ? 2048 : 4096;
+  long long target_a = 64;
+  long long target_b = esize >= 16 ? 32 : 64;
   p->a_dims[0] = a;
   p->na = 1;
   p->b_dims[0] = b;
   p->nb = 1;
-  {
-    long long span = p->ext[a];
-    while (span < target_a) {
+  // Grow a run along its chain: each next dim's stride on that side equals the
+  // run's span so far; a dim of the other chain ends it.
+  auto grow_a = [&](long long target) {
+    long long span = 1;
+    for (int i = 0; i < p->na; ++i) span *= p->ext[p->a_dims[i]];
+    while (span < target && p->na < kMaxDims) {
       int next = -1;
       for (int k = 0; k < p->n; ++k) {
-        if (p->ds[k] == span && !move_chain_contains(p->a_dims, p->na, k) && k != b) next = k;
+        if (p->ds[k] == span && !move_chain_contains(p->a_dims, p->na, k) &&
+            !move_chain_contains(p->b_dims, p->nb, k))
+          next = k;
       }
       if (next < 0) break;
       p->a_dims[p->na++] = next;
       span *= p->ext[next];
     }
-  }
-  {
-    long long span = p->ext[b];
-    while (span < target_b) {
+    return span;
+  };
+  auto grow_b = [&](long long target) {
+    long long span = 1;
+    for (int i = 0; i < p->nb; ++i) span *= p->ext[p->b_dims[i]];
+    while (span < target && p->nb < kMaxDims) {
       int next = -1;
       for (int k = 0; k < p->n; ++k) {
         if (p->ss[k] == span && !move_chain_contains(p->b_dims, p->nb, k) &&
@@ -216,6 +230,35 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
       if (next < 0) break;
       p->b_dims[p->nb++] = next;
       span *= p->ext[next];
+    }
+    return span;
+  };
+  auto pow2_floor = [](long long v) {
+    long long r = 1;
+    while (r * 2 <= v) r *= 2;
+    return r;
+  };
+  auto fits = [&](long long la, long long lb) {
+    return la <= kMoveRunMax && lb <= kMoveRunMax && la * lb <= budget &&
+           la * (lb + 1) * esize <= kMoveTileBytes;
+  };
+  const long long span_a = grow_a(target_a);
+  const long long span_b = grow_b(target_b);
+  const long long run_a = span_a < target_a ? span_a : target_a;
+  const long long run_b = span_b < target_b ? span_b : target_b;
+  if (run_b < target_b) {
+    long long t = pow2_floor(budget / run_b);
+    while (t > target_a && !fits(t, run_b)) t /= 2;
+    if (t > target_a) {
+      grow_a(t);
+      target_a = t;
+    }
+  } else if (run_a < target_a) {
+    long long t = pow2_floor(budget / run_a);
+    while (t > target_b && !fits(run_a, t)) t /= 2;
+    if (t > target_b) {
+      grow_b(t);
+      target_b = t;
     }
   }
   // Tile the last dim of each chain so that the run stays near its target.

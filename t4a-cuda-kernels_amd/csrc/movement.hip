@@ -21,10 +21,10 @@ namespace t4a {
 namespace {
 
 // One LDS arena per block, shared by every payload width's instantiation.
-// Movement: index tables (2 x 64 offsets) plus the largest tile, 64 x 65
-// payloads of 8 bytes or 64 x 33 of 16 bytes. Transpose: one tile of
-// TransposeShape below, at most 128 x 65 8-byte payloads.
-constexpr int kMoveLdsBytes = 128 * 8 + 64 * 33 * 16;
+// Movement: two run-offset tables of kMoveRunMax entries plus the largest padded
+// tile, kMoveTileBytes (128 x 33 payloads of 8 bytes, 64 x 33 of 16 bytes).
+// Transpose: one tile of TransposeShape below, at most 128 x 65 8-byte payloads.
+constexpr int kMoveLdsBytes = 2 * kMoveRunMax * 8 + kMoveTileBytes;
 constexpr int kTransposeLdsBytes = 128 * 65 * 8;
 
 // ---- tiled transpose ---------------------------------------------------------------
@@ -377,7 +377,7 @@ __host__ __device__ inline void tile_vectorizable(const MovePlan& p, int v, cons
 // LDS layout of a tiled block: the two run-offset tables, then the tile.
 __device__ __forceinline__ void tile_tables(const MovePlan& p, unsigned char* lds) {
   long long* src_a = reinterpret_cast<long long*>(lds);
-  long long* dst_b = src_a + 64;
+  long long* dst_b = src_a + kMoveRunMax;
   for (int i = threadIdx.x; i < p.la; i += blockDim.x)
     src_a[i] = chain_offset(p, p.a_dims, p.na, p.a_tile, p.ss, i);
   for (int j = threadIdx.x; j < p.lb; j += blockDim.x)
@@ -390,8 +390,9 @@ __device__ __forceinline__ void move_tiled_as(void* dst, const void* src, const 
                                               unsigned char* lds) {
   tile_tables(p, lds);
   const long long* src_a = reinterpret_cast<const long long*>(lds);
-  move_tiles<P, VL, VS>(static_cast<P*>(dst), static_cast<const P*>(src), p, src_a, src_a + 64,
-                        reinterpret_cast<P*>(lds + 128 * sizeof(long long)));
+  move_tiles<P, VL, VS>(static_cast<P*>(dst), static_cast<const P*>(src), p, src_a,
+                        src_a + kMoveRunMax,
+                        reinterpret_cast<P*>(lds + 2 * kMoveRunMax * sizeof(long long)));
 }
 
 template <typename P>
