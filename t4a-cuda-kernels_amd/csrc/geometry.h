@@ -540,6 +540,10 @@ struct LeanPlan {
   int last_len;
   long long chunk_len;
   long long out_axis_stride;
+  // Equal chunks laid end to end in cube order on both sides (an inner axis
+  // of a compact input, compact partials): cube c's chunk starts at
+  // in_offset + c * chunk_len and its partial at out_offset + c * out_axis_stride.
+  bool linear;
 };
 
 T4A_HD LeanPlan lean_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
@@ -558,6 +562,9 @@ T4A_HD LeanPlan lean_plan(const PartialsPlan& p, long long splits, long long chu
   lp.last_len = static_cast<int>(rd.axis_len - (splits - 1) * chunk_len);
   lp.chunk_len = chunk_len;
   lp.out_axis_stride = rd.out_axis_stride;
+  lp.linear = rd.n <= 1 && lp.last_len == chunk_len &&
+              (rd.n == 0 ||
+               (rd.is[0] == splits * chunk_len && rd.os[0] == splits * rd.out_axis_stride));
   return lp;
 }
 

@@ -413,9 +413,9 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
 // join one at a time -- then the tail element and the xor tree. A float Max /
 // Min first folds in any order with the IEEE maximum / minimum and takes the
 // exact order only when the plane's result is a NaN.
-template <typename Fold, typename T, int K>
+template <typename Fold, typename T, int K, bool Linear>
 __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in_ptr,
-                                              const LeanPlan& lp, long long cubes, Fold f) {
+                                              const LeanPlan& lp, unsigned int cubes, Fold f) {
   constexpr int V = VecLanes<T>::value;
   constexpr int W = kWarp;
   // The block size is the launcher's constant kBlock: reading blockDim would
@@ -425,42 +425,62 @@ __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in
   T* partials = static_cast<T*>(partials_ptr);
   const T* in = static_cast<const T*>(in_ptr);
   const int lane = threadIdx.x % W;
-  const long long planes = static_cast<long long>(gridDim.x) * kPlanes;
-  for (long long cube = static_cast<long long>(blockIdx.x) * kPlanes + threadIdx.x / W;
-       cube < cubes; cube += planes) {
-    // cube = o * splits + split; o over the fused dims, first dim fastest.
-    const unsigned int c32 = static_cast<unsigned int>(cube);
-    unsigned int o = div_by(c32, lp.splits);
-    const unsigned int split = c32 - o * lp.splits.d;
-    long long ib = lp.in_offset;
-    long long pb = lp.out_offset;
+  // 32-bit cube indices: the planner bounds the cube count below 2^31. The
+  // planned grid gives each plane one cube; the stride over the grid (which
+  // reads gridDim) comes only after it.
+  unsigned int cube = blockIdx.x * kPlanes + threadIdx.x / W;
+  if (cube >= cubes) return;
+  for (;; cube += gridDim.x * kPlanes) {
+    if (cube >= cubes) break;
+    const T* chunk;
+    long long pidx;
+    int len;
+    unsigned int split = 0;
+    if constexpr (Linear) {
+      chunk = in + lp.in_offset + static_cast<long long>(cube) * lp.chunk_len;
+      pidx = lp.out_offset + static_cast<long long>(cube) * lp.out_axis_stride;
+      len = static_cast<int>(lp.chunk_len);
+    } else {
+      // cube = o * splits + split; o over the fused dims, first dim fastest.
+      unsigned int o = div_by(cube, lp.splits);
+      split = cube - o * lp.splits.d;
+      long long ib = lp.in_offset;
+      long long pb = lp.out_offset;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      if (k < lp.n) {
-        unsigned int c = o;
-        if (k + 1 < lp.n) {
-          const unsigned int q = div_by(o, lp.ext[k]);
-          c = o - q * lp.ext[k].d;
-          o = q;
+      for (int k = 0; k < 3; ++k) {
+        if (k < lp.n) {
+          unsigned int c = o;
+          if (k + 1 < lp.n) {
+            const unsigned int q = div_by(o, lp.ext[k]);
+            c = o - q * lp.ext[k].d;
+            o = q;
+          }
+          ib += static_cast<long long>(c) * lp.is[k];
+          pb += static_cast<long long>(c) * lp.os[k];
         }
-        ib += static_cast<long long>(c) * lp.is[k];
-        pb += static_cast<long long>(c) * lp.os[k];
       }
+      chunk = in + ib + static_cast<long long>(split) * lp.chunk_len;
+      pidx = pb + static_cast<long long>(split) * lp.out_axis_stride;
+      len = split + 1 == lp.splits.d ? lp.last_len : static_cast<int>(lp.chunk_len);
     }
-    const T* chunk = in + ib + static_cast<long long>(split) * lp.chunk_len;
-    const int len = split + 1 == lp.splits.d ? lp.last_len : static_cast<int>(lp.chunk_len);
     const int groups = len / V;
     const int tail = groups * V;
+    // Every load is unconditional -- a group past the chunk reloads group
+    // `lane`, the tail of a lane without one reloads element 0 -- so no branch
+    // separates them and all are in flight before the first wait; the folds
+    // below skip the stand-ins.
     Group<T, V> b[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      if (k == 0 || lane + k * W < groups) {
-        const Vec<T, V> x = nt_load<T, V>(chunk + (lane + k * W) * V);
-        __builtin_memcpy(&b[k], &x, sizeof(b[k]));
-      }
+      const int g = k == 0 || lane + k * W < groups ? lane + k * W : lane;
+      const Vec<T, V> x = nt_load<T, V>(chunk + g * V);
+      __builtin_memcpy(&b[k], &x, sizeof(b[k]));
     }
+    // The tail (len mod V elements, lanes below it) is loaded only by planes
+    // whose chunk has one: usually none does.
     const bool has_tail = lane < len - tail;
-    const T t = has_tail ? chunk[tail + lane] : b[0].x[0];
+    T t = b[0].x[0];
+    if (len != tail && has_tail) t = chunk[tail + lane];
     auto exact = [&]() {
       T acc = group_value<Fold, T, V>(b[0], f);
 #pragma unroll
@@ -475,20 +495,22 @@ __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in
     if constexpr (!std::is_void_v<Fast>) {
       // Without a NaN any order gives the exact result; the tail element and
       // unloaded groups repeat b[0].x[0], which an extremum ignores.
+      // The stand-in loads repeat group `lane` and element 0 of the chunk
+      // (already among the lane's elements or the plane's), which an extremum
+      // ignores.
       const Fast g;
-      T acc = t;
+      T acc = has_tail ? t : b[0].x[0];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const bool in_range = k == 0 || lane + k * W < groups;
 #pragma unroll
-        for (int c = 0; c < V; ++c) acc = g.combine(acc, in_range ? b[k].x[c] : b[0].x[0]);
+        for (int c = 0; c < V; ++c) acc = g.combine(acc, b[k].x[c]);
       }
       reduced = plane_tree(acc, W, g);
       if (reduced != reduced) reduced = exact();
     } else {
       reduced = exact();
     }
-    if (lane == 0) partials[pb + static_cast<long long>(split) * lp.out_axis_stride] = reduced;
+    if (lane == 0) partials[pidx] = reduced;
   }
 }
 
@@ -574,11 +596,11 @@ __device__ __forceinline__ void fold_lane_rows(const char* base, long long step,
   auto at = [&](int k) {
     return reinterpret_cast<const T*>(base + k * step + lane_off);
   };
+  // Unconditional loads (a row past the chunk reloads row q0) keep every
+  // load of a step in flight before the first wait.
   Vec<T, N> v[kStep];
 #pragma unroll
-  for (int k = 0; k < kStep; ++k) {
-    if (k == 0 || q0 + k * kWarp < len) v[k] = load_n<T, N>(at(k));
-  }
+  for (int k = 0; k < kStep; ++k) v[k] = load_n<T, N>(at(k == 0 || q0 + k * kWarp < len ? k : 0));
 #pragma unroll
   for (int c = 0; c < N; ++c) acc[c] = f.seed(v[0].v[c]);
 #pragma unroll
@@ -590,9 +612,7 @@ __device__ __forceinline__ void fold_lane_rows(const char* base, long long step,
   }
   for (int b = kStep; q0 + b * kWarp < len; b += kStep) {
 #pragma unroll
-    for (int k = 0; k < kStep; ++k) {
-      if (q0 + (b + k) * kWarp < len) v[k] = load_n<T, N>(at(b + k));
-    }
+    for (int k = 0; k < kStep; ++k) v[k] = load_n<T, N>(at(q0 + (b + k) * kWarp < len ? b + k : 0));
 #pragma unroll
     for (int k = 0; k < kStep; ++k) {
       if (q0 + (b + k) * kWarp < len) {
@@ -933,15 +953,12 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <typename T, int K>
+// One kernel per (element type, batch slots, fold, linear walk): the fold is
+// chosen on the host, so each kernel carries one fold's code only.
+template <typename T, int K, typename Fold, bool Linear>
 __global__ void __launch_bounds__(kBlock)
-    partials_lean_kernel(void* partials, const void* in, int op, LeanPlan lp, long long cubes) {
-  if constexpr (VecLanes<T>::value > 0) {
-    dispatch_fold<T>(op, [&](auto fold) {
-      if constexpr (decltype(fold)::kRegroup)
-        partials_lean<decltype(fold), T, K>(partials, in, lp, cubes, fold);
-    });
-  }
+    partials_lean_kernel(void* partials, const void* in, LeanPlan lp, unsigned int cubes) {
+  partials_lean<Fold, T, K, Linear>(partials, in, lp, cubes, Fold{});
 }
 
 template <typename T, int CPL>
@@ -1067,6 +1084,58 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
   });
 }
 
+namespace {
+
+// The lean pass-1 kernel for (K, fold, linear), all chosen on the host.
+template <typename T, int K, typename Fold>
+void launch_lean_k(bool linear, dim3 grid, dim3 block, hipStream_t s, void* partials,
+                   const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+  if (linear)
+    hipLaunchKernelGGL((t4a::partials_lean_kernel<T, K, Fold, true>), grid, block, 0, s,
+                       partials, in, lp, cubes);
+  else
+    hipLaunchKernelGGL((t4a::partials_lean_kernel<T, K, Fold, false>), grid, block, 0, s,
+                       partials, in, lp, cubes);
+}
+
+template <typename T, typename Fold>
+void launch_lean_fold(int k, bool linear, dim3 grid, dim3 block, hipStream_t s, void* partials,
+                      const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+  switch (k) {
+    case 1: launch_lean_k<T, 1, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
+    case 2: launch_lean_k<T, 2, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
+    case 3: launch_lean_k<T, 3, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
+    default: launch_lean_k<T, 4, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
+  }
+}
+
+// The lean mapping serves the regroupable folds (every op but PROD) of the
+// reference's matrix for T.
+template <typename T>
+void launch_lean(int k, int op, bool linear, dim3 grid, dim3 block, hipStream_t s,
+                 void* partials, const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+  constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
+  switch (op) {
+    case T4A_CUDA_REDUCE_SUM:
+      launch_lean_fold<T, t4a::SumFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      break;
+    case T4A_CUDA_REDUCE_SUM_SQUARES:
+      if constexpr (kFloat)
+        launch_lean_fold<T, t4a::SumSquaresFold>(k, linear, grid, block, s, partials, in, lp,
+                                                 cubes);
+      break;
+    case T4A_CUDA_REDUCE_MAX:
+      launch_lean_fold<T, t4a::MaxFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      break;
+    case T4A_CUDA_REDUCE_MIN:
+      launch_lean_fold<T, t4a::MinFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      break;
+    default: break;
+  }
+}
+
+}  // namespace
+
 extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
                                        const t4a_cuda_layout* partials_layout,
                                        const t4a_cuda_layout* in_layout, int axis,
@@ -1107,25 +1176,10 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
     using T = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (lean > 0) {
-      const t4a::LeanPlan lp = t4a::lean_plan(pp, splits, chunk_len);
-      const long long cubes = output_len * splits;
-      switch (lean) {
-        case 1:
-          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 1>), grid, block, 0, s, partials, in,
-                             op, lp, cubes);
-          break;
-        case 2:
-          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 2>), grid, block, 0, s, partials, in,
-                             op, lp, cubes);
-          break;
-        case 3:
-          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 3>), grid, block, 0, s, partials, in,
-                             op, lp, cubes);
-          break;
-        default:
-          hipLaunchKernelGGL((t4a::partials_lean_kernel<T, 4>), grid, block, 0, s, partials, in,
-                             op, lp, cubes);
-          break;
+      if constexpr (t4a::VecLanes<T>::value > 0) {
+        const t4a::LeanPlan lp = t4a::lean_plan(pp, splits, chunk_len);
+        const unsigned int cubes = static_cast<unsigned int>(output_len * splits);
+        launch_lean<T>(lean, op, lp.linear, grid, block, s, partials, in, lp, cubes);
       }
     } else if (stream_mode) {
       hipLaunchKernelGGL(t4a::partials_stream_kernel<T>, grid, block, 0,
