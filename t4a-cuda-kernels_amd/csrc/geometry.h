@@ -26,6 +26,9 @@ namespace t4a {
 // Threads per block of the MI355X launches this library plans (four 64-lane
 // wavefronts; the tiled transpose runs eight).
 constexpr int kBlock = 256;
+// Unit reductions over a few thousand outputs (combine passes) run one
+// wavefront per block so that they spread over more CUs.
+constexpr int kUnitSmallBlock = 64;
 constexpr int kTransposeBlock = 512;
 constexpr int kWave = 64;
 // Lanes of a reference "warp": planes wider than this cross it (reduce.cu:140).

@@ -198,7 +198,9 @@ int strategy_for(long long reduce_len, unsigned w) {
 
 // Reference launch_for (src/lib.rs:3243-3286), with this library's UNIT geometry:
 // a unit reduction's fold does not depend on the block, so it runs 256-thread
-// blocks; a PLANE block is the plane.
+// blocks, or 64-thread ones when that still leaves fewer than 1024 blocks (a
+// combine pass over a few thousand outputs then spreads over more CUs); a
+// PLANE block is the plane.
 int launch_for(int strategy, long long output_len, unsigned w, t4a_launch* out) {
   if (strategy == T4A_CUDA_REDUCE_UNIT) {
     if (output_len < 0) return T4A_ERR_NEGATIVE_COUNT;
@@ -206,7 +208,9 @@ int launch_for(int strategy, long long output_len, unsigned w, t4a_launch* out) 
         (static_cast<unsigned long long>(output_len) + w - 1) / w;
     if (blocks > UINT32_MAX) return T4A_ERR_LAUNCH_LIMIT;
     if (blocks > kMaxGridX) return T4A_ERR_LAUNCH_LIMIT;
-    set_launch(out, output_len == 0 ? 0 : blocks_for(output_len, kBlock), kBlock, 0);
+    const long long bs = output_len < 1024LL * kBlock ? t4a::kUnitSmallBlock : kBlock;
+    set_launch(out, output_len == 0 ? 0 : blocks_for(output_len, bs), static_cast<unsigned>(bs),
+               0);
     return ok();
   }
   if (output_len < 0 || output_len > static_cast<long long>(UINT32_MAX))

@@ -115,6 +115,33 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
     T acc;
     if constexpr (Vector) {
       constexpr int V = VecLanes<T>::value;
+      // Short axes keep every load in registers: only in the small-output
+      // instance (combine passes), whose occupancy does not matter; the
+      // registers would cost a many-output reduction its occupancy.
+      constexpr int kShort = 16;  // groups held at once on a short axis
+      if (BS == kUnitSmallBlock && len <= kShort * V) {
+        // A short axis (a combine pass over a few dozen partials): every load
+        // is issued before the first fold, then the fold runs in order.
+        const int groups = static_cast<int>(len / V);
+        Group<T, V> g[kShort];
+#pragma unroll
+        for (int k = 0; k < kShort; ++k) {
+          if (k < groups) g[k] = reinterpret_cast<const Group<T, V>*>(x)[k];
+        }
+        acc = f.seed(g[0].x[0]);
+#pragma unroll
+        for (int c = 1; c < V; ++c) acc = f.fold(acc, g[0].x[c]);
+#pragma unroll
+        for (int k = 1; k < kShort; ++k) {
+          if (k < groups) {
+#pragma unroll
+            for (int c = 0; c < V; ++c) acc = f.fold(acc, g[k].x[c]);
+          }
+        }
+        for (long long i = static_cast<long long>(groups) * V; i < len; ++i) acc = f.fold(acc, x[i]);
+        out[ob] = acc;
+        continue;
+      }
       const Group<T, V> g0 = *reinterpret_cast<const Group<T, V>*>(x);
       acc = f.seed(g0.x[0]);
 #pragma unroll
@@ -127,9 +154,23 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
       }
       for (; i < len; ++i) acc = f.fold(acc, x[i]);
     } else {
-      acc = f.seed(x[0]);
+      constexpr int kShort = 32;  // elements held at once on a short axis
+      if (BS == kUnitSmallBlock && len <= kShort) {
+        T v[kShort];
+#pragma unroll
+        for (int k = 0; k < kShort; ++k) {
+          if (k < len) v[k] = x[k * stride];
+        }
+        acc = f.seed(v[0]);
+#pragma unroll
+        for (int k = 1; k < kShort; ++k) {
+          if (k < len) acc = f.fold(acc, v[k]);
+        }
+      } else {
+        acc = f.seed(x[0]);
 #pragma unroll 4
-      for (long long i = 1; i < len; ++i) acc = f.fold(acc, x[i * stride]);
+        for (long long i = 1; i < len; ++i) acc = f.fold(acc, x[i * stride]);
+      }
     }
     out[ob] = acc;
   }
@@ -921,12 +962,12 @@ __global__ void __launch_bounds__(512)
   reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds);
 }
 
-// UNIT with the planner's kBlock-thread blocks.
-template <typename T>
-__global__ void __launch_bounds__(kBlock)
+// UNIT with the planner's blocks of BS threads.
+template <typename T, int BS>
+__global__ void __launch_bounds__(BS)
     reduce_unit_kernel(void* out, const void* in, int op, ReduceDims rd, long long output_len) {
   dispatch_fold<T>(op, [&](auto fold) {
-    unit_body<decltype(fold), T, kBlock>(out, in, rd, output_len, fold);
+    unit_body<decltype(fold), T, BS>(out, in, rd, output_len, fold);
   });
 }
 
@@ -1073,7 +1114,11 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
     using T = std::remove_pointer_t<decltype(tag)>;
     const unsigned threads = block.x * block.y * block.z;
     if (strategy == T4A_CUDA_REDUCE_UNIT && threads == static_cast<unsigned>(t4a::kBlock)) {
-      hipLaunchKernelGGL(t4a::reduce_unit_kernel<T>, grid, block, 0,
+      hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kBlock>), grid, block, 0,
+                         static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
+    } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
+               threads == static_cast<unsigned>(t4a::kUnitSmallBlock)) {
+      hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kUnitSmallBlock>), grid, block, 0,
                          static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
     } else {
       hipLaunchKernelGGL(t4a::reduce_kernel<T>, grid, block, 0,

@@ -194,7 +194,12 @@ def test_reduction_geometry_and_shapes():
     assert launch.grid == (8, 1, 1) and launch.block == (32, 1, 1)  # one plane per output
     inp, out = reduced([4, 4, 2], 1)
     launch = t.plan_reduce(DType.F32, ReduceOp.Sum, ReduceStrategy.Unit, out, 8, inp, 32, 1, 8)
-    assert launch.grid == (1, 1, 1) and launch.block == (256, 1, 1)
+    # this build's unit geometry: one-wavefront blocks below 1024 * 256 outputs
+    assert launch.grid == (1, 1, 1) and launch.block == (64, 1, 1)
+    inp, out = reduced([4, 4, 300_000], 1)
+    launch = t.plan_reduce(DType.F32, ReduceOp.Sum, ReduceStrategy.Unit, out, 1_200_000, inp,
+                           4_800_000, 1, 8)
+    assert launch.grid == (4688, 1, 1) and launch.block == (256, 1, 1)
     inp, _ = reduced([4, 64], 1)
     assert err(t.plan_reduce, DType.F32, ReduceOp.Sum, ReduceStrategy.Plane,
                Layout.compact([4]), 4, inp, 256, 1, 32) == Error.RankLength
