@@ -387,6 +387,26 @@ T4A_HD unsigned int div_by(unsigned int x, const FastDiv& f) {
   return (t + x) >> f.shift;
 }
 
+// A unit reduction whose axis is one 16-byte group (V <= len < 2V contiguous
+// elements of a 4- or 8-byte real or integer type, every output's start a
+// multiple of V): a thread takes kUnitOutputsPerThread outputs at once, their
+// loads issued together.
+constexpr int kUnitOutputsPerThread = 4;
+
+T4A_HD bool unit_one_group(const ReduceDims& rd, int dtype) {
+  const int es = dtype_size(dtype);
+  const bool real_or_int = dtype == T4A_CUDA_F32 || dtype == T4A_CUDA_F64 ||
+                           dtype == T4A_CUDA_I32 || dtype == T4A_CUDA_I64;
+  if (!real_or_int) return false;
+  const long long v = 16 / es;
+  if (rd.axis_stride != 1 || rd.axis_len < v || rd.axis_len >= 2 * v || rd.in_offset % v != 0)
+    return false;
+  for (int k = 0; k < rd.n; ++k) {
+    if (rd.is[k] % v != 0) return false;
+  }
+  return true;
+}
+
 // Element types the sideways pass-1 mappings serve (real and integer; complex
 // keeps the plane mapping).
 T4A_HD bool sideways_dtype(int dtype) {

@@ -456,7 +456,17 @@ int t4a_plan_reduce(int dtype, int op, int strategy, const t4a_cuda_layout* out_
     return T4A_ERR_STRATEGY_MISMATCH;
   if (strategy == T4A_CUDA_REDUCE_PLANE && reduce_len < static_cast<long long>(plane_width))
     return T4A_ERR_STRATEGY_MISMATCH;
-  return launch_for(strategy, output_len, plane_width, launch);
+  if (int s = launch_for(strategy, output_len, plane_width, launch)) return s;
+  // A one-group axis in kBlock-thread blocks: threads take several outputs.
+  if (strategy == T4A_CUDA_REDUCE_UNIT && output_len > 0 &&
+      launch->block[0] == static_cast<unsigned>(kBlock)) {
+    t4a::ReduceDims rd;
+    t4a::reduce_dims(&rd, *out_layout, *in_layout, static_cast<int>(axis));
+    if (t4a::unit_one_group(rd, dtype))
+      set_launch(launch, blocks_for(output_len, kBlock * t4a::kUnitOutputsPerThread), kBlock,
+                 0);
+  }
+  return ok();
 }
 
 // Reference plan_reduce_partials (src/lib.rs:3340-3431). A 32-lane plan runs

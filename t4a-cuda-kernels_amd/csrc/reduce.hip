@@ -176,6 +176,45 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
   }
 }
 
+// UNIT over a one-group axis (unit_one_group) in kBlock blocks: each thread
+// takes outputs o, o + G, o + 2G, o + 3G (G the grid's thread count), issues
+// their 16-byte loads together, then folds each output serially from element 0.
+template <typename Fold, typename T>
+__device__ __forceinline__ void unit_outputs_grouped(T* __restrict__ out,
+                                                     const T* __restrict__ in,
+                                                     const ReduceDims& rd, long long output_len,
+                                                     Fold f) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int U = kUnitOutputsPerThread;
+  const long long len = rd.axis_len;
+  const long long gstride = static_cast<long long>(gridDim.x) * kBlock;
+  for (long long o0 = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; o0 < output_len;
+       o0 += U * gstride) {
+    Group<T, V> g[U];
+    long long ob[U];
+    const T* xs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long o = o0 + u * gstride;
+      long long ib;
+      decode_output(rd, o < output_len ? o : o0, &ib, &ob[u]);  // past the end: o0 again
+      xs[u] = in + ib;
+      const Vec<T, V> x = nt_load<T, V>(xs[u]);
+      __builtin_memcpy(&g[u], &x, sizeof(g[u]));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (o0 + u * gstride < output_len) {
+        T acc = f.seed(g[u].x[0]);
+#pragma unroll
+        for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
+        for (long long i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
+        out[ob[u]] = acc;
+      }
+    }
+  }
+}
+
 template <typename Fold, typename T, int BS>
 __device__ __forceinline__ void unit_body(void* out, const void* in, const ReduceDims& rd,
                                           long long output_len, Fold f) {
@@ -188,6 +227,12 @@ __device__ __forceinline__ void unit_body(void* out, const void* in, const Reduc
 #pragma unroll
     for (int k = 0; k < kMaxDims; ++k) vector = vector && (k >= rd.n || rd.is[k] % V == 0);
     if (vector) {
+      if constexpr (BS == kBlock) {
+        if (rd.axis_len < 2 * V) {
+          unit_outputs_grouped<Fold, T>(o, x, rd, output_len, f);
+          return;
+        }
+      }
       unit_outputs<Fold, T, true, BS>(o, x, rd, output_len, f);
       return;
     }

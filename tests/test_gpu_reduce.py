@@ -222,6 +222,20 @@ def test_special_values():
             run(dtype, op, t.Layout.compact(ext), 0, t.Layout.compact([1, 3]), 32, data)
 
 
+@pytest.mark.parametrize("dtype", [F32, F64, I32, I64], ids=lambda d: d.name)
+def test_unit_one_group_axes_many_outputs(dtype):
+    """Unit reductions over a one-group axis (4..7 elements of 4 bytes, 2..3 of 8)
+    with enough outputs for the four-outputs-per-thread mapping, ragged count."""
+    rng = np.random.default_rng(12 + int(dtype))
+    v = 16 // dtype.size
+    for length in range(v, 2 * v):
+        for op in (Sum, Prod, Max, Min):
+            if not op.supports(dtype):
+                continue
+            compact_case(dtype, op, (300_007, length), 1, 32, rng,
+                         explicit=(t.ReduceStrategy.Unit, 32))
+
+
 def test_extrema_nan_payloads_bit_exact():
     """Max / Min select an operand, so their results are exact bytes even for NaN
     payloads: several payloads (quiet, signalling, negative) in one chunk, in
