@@ -387,6 +387,46 @@ T4A_HD unsigned int div_by(unsigned int x, const FastDiv& f) {
   return (t + x) >> f.shift;
 }
 
+// The unit kernels' compact plan: at most three fused output dims with
+// precomputed divisors, 32-bit output indices. `vector`: the axis is contiguous
+// and every output's start a multiple of v = 16 / esize elements (the launcher
+// also checks the pointer's alignment).
+struct UnitPlan {
+  long long in_offset;
+  long long out_offset;
+  long long axis_stride;
+  long long is[3];
+  long long os[3];
+  FastDiv ext[3];
+  int n;
+  int axis_len;
+  bool vector;
+};
+
+T4A_HD bool unit_plan_fits(const ReduceDims& rd, long long output_len) {
+  return rd.n <= 3 && output_len < (1ll << 31) && rd.axis_len < (1ll << 31);
+}
+
+T4A_HD UnitPlan unit_plan(const ReduceDims& rd, int v, bool aligned) {
+  UnitPlan up;
+  up.in_offset = rd.in_offset;
+  up.out_offset = rd.out_offset;
+  up.axis_stride = rd.axis_stride;
+  up.axis_len = static_cast<int>(rd.axis_len);
+  up.n = rd.n;
+  for (int k = 0; k < 3; ++k) {
+    const bool used = k < rd.n;
+    up.is[k] = used ? rd.is[k] : 0;
+    up.os[k] = used ? rd.os[k] : 0;
+    up.ext[k] = fast_div(used ? static_cast<unsigned int>(rd.ext[k]) : 1u);
+  }
+  bool vector = v > 0 && aligned && rd.axis_stride == 1 && rd.axis_len >= v &&
+                rd.in_offset % v == 0;
+  for (int k = 0; k < rd.n; ++k) vector = vector && rd.is[k] % v == 0;
+  up.vector = vector;
+  return up;
+}
+
 // A unit reduction whose axis is one 16-byte group (V <= len < 2V contiguous
 // elements of a 4- or 8-byte real or integer type, every output's start a
 // multiple of V): a thread takes kUnitOutputsPerThread outputs at once, their

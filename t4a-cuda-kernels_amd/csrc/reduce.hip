@@ -240,6 +240,141 @@ __device__ __forceinline__ void unit_body(void* out, const void* in, const Reduc
   unit_outputs<Fold, T, false, BS>(o, x, rd, output_len, f);
 }
 
+// ---- t4a_cuda_reduce: UNIT on a compact plan ----------------------------------------
+// The same folds as unit_outputs / unit_outputs_grouped with the output decode
+// on a UnitPlan (32-bit quotients by precomputed divisors) and the fold fixed
+// at compile time: the general ReduceDims decode over eight dims keeps too many
+// scalar registers live for a kernel whose wavefronts are short-lived.
+__device__ __forceinline__ void unit_decode(const UnitPlan& up, unsigned int o, long long* ib,
+                                            long long* ob) {
+  long long i = up.in_offset;
+  long long w = up.out_offset;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (k < up.n) {
+      unsigned int c = o;
+      if (k + 1 < up.n) {
+        const unsigned int q = div_by(o, up.ext[k]);
+        c = o - q * up.ext[k].d;
+        o = q;
+      }
+      i += static_cast<long long>(c) * up.is[k];
+      w += static_cast<long long>(c) * up.os[k];
+    }
+  }
+  *ib = i;
+  *ob = w;
+}
+
+template <typename Fold, typename T, int BS>
+__device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restrict__ in,
+                                          const UnitPlan& up, unsigned int output_len, Fold f) {
+  const int len = up.axis_len;
+  const unsigned int gstride = gridDim.x * BS;
+  if constexpr (VecLanes<T>::value > 0) {
+    constexpr int V = VecLanes<T>::value;
+    if (up.vector) {
+      if constexpr (BS == kBlock) {
+        if (len < 2 * V) {
+          // one group per output: four outputs a grid-stride apart per thread
+          constexpr int U = kUnitOutputsPerThread;
+          for (unsigned int o0 = blockIdx.x * BS + threadIdx.x; o0 < output_len;
+               o0 += U * gstride) {
+            Group<T, V> g[U];
+            long long ob[U];
+            const T* xs[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+              const unsigned int o = o0 + u * gstride;
+              long long ib;
+              unit_decode(up, o < output_len ? o : o0, &ib, &ob[u]);
+              xs[u] = in + ib;
+              const Vec<T, V> x = nt_load<T, V>(xs[u]);
+              __builtin_memcpy(&g[u], &x, sizeof(g[u]));
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+              if (o0 + u * gstride < output_len) {
+                T acc = f.seed(g[u].x[0]);
+#pragma unroll
+                for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
+                for (int i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
+                out[ob[u]] = acc;
+              }
+            }
+          }
+          return;
+        }
+      }
+      for (unsigned int o = blockIdx.x * BS + threadIdx.x; o < output_len; o += gstride) {
+        long long ib, ob;
+        unit_decode(up, o, &ib, &ob);
+        const T* x = in + ib;
+        const Group<T, V>* g = reinterpret_cast<const Group<T, V>*>(x);
+        const int groups = len / V;
+        T acc;
+        constexpr int kShort = 16;
+        if (BS != kBlock && groups <= kShort) {
+          // a short axis (combine passes): every load before the first fold
+          Group<T, V> v[kShort];
+#pragma unroll
+          for (int k = 0; k < kShort; ++k) {
+            if (k < groups) v[k] = g[k];
+          }
+          acc = f.seed(v[0].x[0]);
+#pragma unroll
+          for (int c = 1; c < V; ++c) acc = f.fold(acc, v[0].x[c]);
+#pragma unroll
+          for (int k = 1; k < kShort; ++k) {
+            if (k < groups) {
+#pragma unroll
+              for (int c = 0; c < V; ++c) acc = f.fold(acc, v[k].x[c]);
+            }
+          }
+        } else {
+          const Group<T, V> g0 = g[0];
+          acc = f.seed(g0.x[0]);
+#pragma unroll
+          for (int c = 1; c < V; ++c) acc = f.fold(acc, g0.x[c]);
+          for (int k = 1; k < groups; ++k) {
+            const Group<T, V> gk = g[k];
+#pragma unroll
+            for (int c = 0; c < V; ++c) acc = f.fold(acc, gk.x[c]);
+          }
+        }
+        for (int i = groups * V; i < len; ++i) acc = f.fold(acc, x[i]);
+        out[ob] = acc;
+      }
+      return;
+    }
+  }
+  const long long stride = up.axis_stride;
+  for (unsigned int o = blockIdx.x * BS + threadIdx.x; o < output_len; o += gstride) {
+    long long ib, ob;
+    unit_decode(up, o, &ib, &ob);
+    const T* x = in + ib;
+    T acc;
+    constexpr int kShort = 32;
+    if (BS != kBlock && len <= kShort) {
+      T v[kShort];
+#pragma unroll
+      for (int k = 0; k < kShort; ++k) {
+        if (k < len) v[k] = x[k * stride];
+      }
+      acc = f.seed(v[0]);
+#pragma unroll
+      for (int k = 1; k < kShort; ++k) {
+        if (k < len) acc = f.fold(acc, v[k]);
+      }
+    } else {
+      acc = f.seed(x[0]);
+#pragma unroll 4
+      for (int i = 1; i < len; ++i) acc = f.fold(acc, x[i * stride]);
+    }
+    out[ob] = acc;
+  }
+}
+
 // ---- t4a_cuda_reduce: PLANE --------------------------------------------------------
 // One plane of W = blockDim.x lanes per output (reference reduce.cu:226-340).
 // W <= 32: the xor tree. W = 64..512: the xor tree inside each 32-lane warp,
@@ -1007,6 +1142,14 @@ __global__ void __launch_bounds__(512)
   reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds);
 }
 
+// UNIT on a compact plan, one kernel per (element type, fold, block size).
+template <typename T, typename Fold, int BS>
+__global__ void __launch_bounds__(BS)
+    reduce_unit_lean_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len) {
+  unit_lean<Fold, T, BS>(static_cast<T*>(out), static_cast<const T*>(in), up, output_len,
+                         Fold{});
+}
+
 // UNIT with the planner's blocks of BS threads.
 template <typename T, int BS>
 __global__ void __launch_bounds__(BS)
@@ -1143,6 +1286,52 @@ using t4a::status_of_last_launch;
 
 }  // namespace
 
+namespace {
+
+// The unit kernel for (fold, block size), both chosen on the host, over the
+// reference's op matrix for T.
+template <typename T, typename Fold>
+void launch_unit_fold(unsigned threads, dim3 grid, dim3 block, hipStream_t s, void* out,
+                      const void* in, const t4a::UnitPlan& up, unsigned int output_len) {
+  if (threads == static_cast<unsigned>(t4a::kBlock))
+    hipLaunchKernelGGL((t4a::reduce_unit_lean_kernel<T, Fold, t4a::kBlock>), grid, block, 0, s,
+                       out, in, up, output_len);
+  else
+    hipLaunchKernelGGL((t4a::reduce_unit_lean_kernel<T, Fold, t4a::kUnitSmallBlock>), grid,
+                       block, 0, s, out, in, up, output_len);
+}
+
+template <typename T>
+void launch_unit_lean(int op, unsigned threads, dim3 grid, dim3 block, hipStream_t s, void* out,
+                      const void* in, const t4a::UnitPlan& up, unsigned int output_len) {
+  constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
+  constexpr bool kOrdered = kFloat || std::is_same_v<T, int> || std::is_same_v<T, long long>;
+  switch (op) {
+    case T4A_CUDA_REDUCE_SUM:
+      launch_unit_fold<T, t4a::SumFold>(threads, grid, block, s, out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_PROD:
+      launch_unit_fold<T, t4a::ProdFold>(threads, grid, block, s, out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_SUM_SQUARES:
+      if constexpr (kFloat)
+        launch_unit_fold<T, t4a::SumSquaresFold>(threads, grid, block, s, out, in, up,
+                                                 output_len);
+      break;
+    case T4A_CUDA_REDUCE_MAX:
+      if constexpr (kOrdered)
+        launch_unit_fold<T, t4a::MaxFold>(threads, grid, block, s, out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_MIN:
+      if constexpr (kOrdered)
+        launch_unit_fold<T, t4a::MinFold>(threads, grid, block, s, out, in, up, output_len);
+      break;
+    default: break;
+  }
+}
+
+}  // namespace
+
 extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int strategy,
                               const t4a_cuda_layout* out_layout,
                               const t4a_cuda_layout* in_layout, int axis, long long output_len,
@@ -1158,7 +1347,15 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
   return with_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
     const unsigned threads = block.x * block.y * block.z;
-    if (strategy == T4A_CUDA_REDUCE_UNIT && threads == static_cast<unsigned>(t4a::kBlock)) {
+    if (strategy == T4A_CUDA_REDUCE_UNIT && t4a::unit_plan_fits(rd, output_len) &&
+        (threads == static_cast<unsigned>(t4a::kBlock) ||
+         threads == static_cast<unsigned>(t4a::kUnitSmallBlock))) {
+      const bool aligned = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+      const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, aligned);
+      launch_unit_lean<T>(op, threads, grid, block, static_cast<hipStream_t>(stream), out, in,
+                          up, static_cast<unsigned int>(output_len));
+    } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
+               threads == static_cast<unsigned>(t4a::kBlock)) {
       hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kBlock>), grid, block, 0,
                          static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
     } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
