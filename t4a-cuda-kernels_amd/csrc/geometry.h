@@ -593,16 +593,20 @@ T4A_HD int lean_slots(const PartialsPlan& p, int dtype, int op, long long splits
 // The lean mapping's own plan: the fused non-axis dims (at most three) with
 // their divisors precomputed, and the split walk.
 struct LeanPlan {
+  // First, next to each other: what a wavefront needs before its first load
+  // (the cube count it tests against, the chunk's place), so that one scalar
+  // load fetches them all.
+  unsigned int cubes;
   long long in_offset;
+  long long chunk_len;
   long long out_offset;
+  long long out_axis_stride;
   long long is[3];
   long long os[3];
   FastDiv ext[3];
   FastDiv splits;
   int n;
   int last_len;
-  long long chunk_len;
-  long long out_axis_stride;
   // Equal chunks laid end to end in cube order on both sides (an inner axis
   // of a compact input, compact partials): cube c's chunk starts at
   // in_offset + c * chunk_len and its partial at out_offset + c * out_axis_stride.
@@ -611,6 +615,7 @@ struct LeanPlan {
 
 T4A_HD LeanPlan lean_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
   LeanPlan lp;
+  lp.cubes = static_cast<unsigned int>(p.units);
   const ReduceDims& rd = p.dims;
   lp.in_offset = rd.in_offset;
   lp.out_offset = rd.out_offset;

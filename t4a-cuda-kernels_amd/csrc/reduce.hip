@@ -636,7 +636,8 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
 // exact order only when the plane's result is a NaN.
 template <typename Fold, typename T, int K, bool Linear>
 __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in_ptr,
-                                              const LeanPlan& lp, unsigned int cubes, Fold f) {
+                                              const LeanPlan& lp, Fold f) {
+  const unsigned int cubes = lp.cubes;
   constexpr int V = VecLanes<T>::value;
   constexpr int W = kWarp;
   // The block size is the launcher's constant kBlock: reading blockDim would
@@ -650,6 +651,11 @@ __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in
   // planned grid gives each plane one cube; the stride over the grid (which
   // reads gridDim) comes only after it.
   unsigned int cube = blockIdx.x * kPlanes + threadIdx.x / W;
+  // The plan's fields are made operands of an empty asm statement ahead of the
+  // exit test: otherwise the compiler sinks their loads past the branch on the
+  // cube count, a second scalar round trip before the first data load.
+  asm volatile("" ::"s"(lp.in_offset), "s"(lp.chunk_len), "s"(lp.out_offset),
+               "s"(lp.out_axis_stride), "s"(in), "s"(partials));
   if (cube >= cubes) return;
   for (;; cube += gridDim.x * kPlanes) {
     if (cube >= cubes) break;
@@ -1186,8 +1192,8 @@ __global__ void __launch_bounds__(256)
 // chosen on the host, so each kernel carries one fold's code only.
 template <typename T, int K, typename Fold, bool Linear>
 __global__ void __launch_bounds__(kBlock)
-    partials_lean_kernel(void* partials, const void* in, LeanPlan lp, unsigned int cubes) {
-  partials_lean<Fold, T, K, Linear>(partials, in, lp, cubes, Fold{});
+    partials_lean_kernel(void* partials, const void* in, LeanPlan lp) {
+  partials_lean<Fold, T, K, Linear>(partials, in, lp, Fold{});
 }
 
 template <typename T, int CPL>
@@ -1376,23 +1382,23 @@ namespace {
 // The lean pass-1 kernel for (K, fold, linear), all chosen on the host.
 template <typename T, int K, typename Fold>
 void launch_lean_k(bool linear, dim3 grid, dim3 block, hipStream_t s, void* partials,
-                   const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+                   const void* in, const t4a::LeanPlan& lp) {
   if (linear)
     hipLaunchKernelGGL((t4a::partials_lean_kernel<T, K, Fold, true>), grid, block, 0, s,
-                       partials, in, lp, cubes);
+                       partials, in, lp);
   else
     hipLaunchKernelGGL((t4a::partials_lean_kernel<T, K, Fold, false>), grid, block, 0, s,
-                       partials, in, lp, cubes);
+                       partials, in, lp);
 }
 
 template <typename T, typename Fold>
 void launch_lean_fold(int k, bool linear, dim3 grid, dim3 block, hipStream_t s, void* partials,
-                      const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+                      const void* in, const t4a::LeanPlan& lp) {
   switch (k) {
-    case 1: launch_lean_k<T, 1, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
-    case 2: launch_lean_k<T, 2, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
-    case 3: launch_lean_k<T, 3, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
-    default: launch_lean_k<T, 4, Fold>(linear, grid, block, s, partials, in, lp, cubes); break;
+    case 1: launch_lean_k<T, 1, Fold>(linear, grid, block, s, partials, in, lp); break;
+    case 2: launch_lean_k<T, 2, Fold>(linear, grid, block, s, partials, in, lp); break;
+    case 3: launch_lean_k<T, 3, Fold>(linear, grid, block, s, partials, in, lp); break;
+    default: launch_lean_k<T, 4, Fold>(linear, grid, block, s, partials, in, lp); break;
   }
 }
 
@@ -1400,22 +1406,21 @@ void launch_lean_fold(int k, bool linear, dim3 grid, dim3 block, hipStream_t s, 
 // reference's matrix for T.
 template <typename T>
 void launch_lean(int k, int op, bool linear, dim3 grid, dim3 block, hipStream_t s,
-                 void* partials, const void* in, const t4a::LeanPlan& lp, unsigned int cubes) {
+                 void* partials, const void* in, const t4a::LeanPlan& lp) {
   constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
   switch (op) {
     case T4A_CUDA_REDUCE_SUM:
-      launch_lean_fold<T, t4a::SumFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      launch_lean_fold<T, t4a::SumFold>(k, linear, grid, block, s, partials, in, lp);
       break;
     case T4A_CUDA_REDUCE_SUM_SQUARES:
       if constexpr (kFloat)
-        launch_lean_fold<T, t4a::SumSquaresFold>(k, linear, grid, block, s, partials, in, lp,
-                                                 cubes);
+        launch_lean_fold<T, t4a::SumSquaresFold>(k, linear, grid, block, s, partials, in, lp);
       break;
     case T4A_CUDA_REDUCE_MAX:
-      launch_lean_fold<T, t4a::MaxFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      launch_lean_fold<T, t4a::MaxFold>(k, linear, grid, block, s, partials, in, lp);
       break;
     case T4A_CUDA_REDUCE_MIN:
-      launch_lean_fold<T, t4a::MinFold>(k, linear, grid, block, s, partials, in, lp, cubes);
+      launch_lean_fold<T, t4a::MinFold>(k, linear, grid, block, s, partials, in, lp);
       break;
     default: break;
   }
@@ -1465,8 +1470,7 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
     if (lean > 0) {
       if constexpr (t4a::VecLanes<T>::value > 0) {
         const t4a::LeanPlan lp = t4a::lean_plan(pp, splits, chunk_len);
-        const unsigned int cubes = static_cast<unsigned int>(output_len * splits);
-        launch_lean<T>(lean, op, lp.linear, grid, block, s, partials, in, lp, cubes);
+        launch_lean<T>(lean, op, lp.linear, grid, block, s, partials, in, lp);
       }
     } else if (stream_mode) {
       hipLaunchKernelGGL(t4a::partials_stream_kernel<T>, grid, block, 0,
