@@ -54,7 +54,7 @@ ROTATE = 3
 # needs a new measurement; until then the entry is left out and traffic is null.
 TRAFFIC: dict[tuple[str, str], dict] = {
     ("c2", "sum_i64_inner"): {"bytes": 538906757, "source": "profiles/traffic_c2_sum_i64_inner.md"},
-    ("c2", "sum_f32_inner"): {"bytes": 269468757, "source": "profiles/traffic_c2_sum_f32_inner.md"},
+    ("c2", "sum_f32_inner"): {"bytes": 269755725, "source": "profiles/traffic_c2_sum_f32_inner.md"},
     ("c2", "sum_f32_outer"): {"bytes": 269531508, "source": "profiles/traffic_c2_sum_f32_outer.md"},
     ("c1big", "transpose_f32_8192"): {"bytes": 537115975, "source": "profiles/traffic_c1big_transpose_f32_8192.md"},
     ("c3", "permute4_F64"): {"bytes": 268721201, "source": "profiles/traffic_c3_permute4_F64.md"},
@@ -136,13 +136,18 @@ def reduction_op(name, dtype, op, in_ext, axis, sets, host) -> Op:
         part = hipmem.DeviceBuffer(pl.element_count() * es)
     else:
         pl, part = None, None
+    # The whole plan through t4a_hip_reduction: one launch where a block can
+    # hold all of an output's chunks and fold their partials itself.
+    joined = plan.kind == "Split" and hip.reduction_joins(plan, sets[0], dtype, op, out_l, in_l,
+                                                          axis, on)
 
     def launch(r):
-        hip.enqueue_reduction(plan, out, sets[r], part, dtype, op, out_l, in_l, axis, on,
-                              _stream())
+        hip.reduction(plan, out, sets[r], part, dtype, op, out_l, in_l, axis, on, _stream())
 
     def dominant(r):
-        if plan.kind == "Split":
+        if joined:
+            launch(r)
+        elif plan.kind == "Split":
             hip.reduce_partials(part, sets[r], dtype, op, pl, in_l, axis, on,
                                 plan.split.splits, plan.split.chunk_len, plan.pass1, _stream())
         else:
@@ -170,9 +175,13 @@ def reduction_op(name, dtype, op, in_ext, axis, sets, host) -> Op:
             width = plan.launch.block[0] if plan.strategy == t.ReduceStrategy.Plane else 32
             orc.reduce(h_out, host, dtype, op, plan.strategy, width, out_l, in_l, axis, on)
 
-    kernel = "reduce_partials" if plan.kind == "Split" else "reduce"
-    return Op(name, kernel, (n + on) * es, launch, dominant,
-              (n + (pl.element_count() if pl else on)) * es, cpu)
+    if joined:  # pass 1 and the combine in one launch: input, partials and finals
+        kernel, dom_bytes = "reduction_joined", (n + pl.element_count() + on) * es
+    elif plan.kind == "Split":
+        kernel, dom_bytes = "reduce_partials", (n + pl.element_count()) * es
+    else:
+        kernel, dom_bytes = "reduce", (n + on) * es
+    return Op(name, kernel, (n + on) * es, launch, dominant, dom_bytes, cpu)
 
 
 def transpose_op(name, dtype, m, n, sets, outs, host) -> Op:

@@ -192,6 +192,26 @@ int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
                             long long splits, long long chunk_len, const t4a_launch* launch,
                             void* stream);
 
+/* A whole reduction_plan (reference src/lib.rs:3457-3528 plans it; its caller
+ * then launches pass 1 and the combine, reduce.cu:813-852 and 765-811): Direct
+ * runs t4a_hip_reduce; Split runs pass 1 into `partials` (the
+ * t4a_reduction_partials_layout of the plan) and the combine into `out`, on
+ * `stream`. A Split plan whose combine is a unit fold over at most 32 partials
+ * of a contiguous, end-to-end chunk layout runs as ONE launch: each block holds
+ * all of an output's chunks and folds their partials in the unit order, so
+ * finals and partials are the two launches' bits. */
+int t4a_hip_reduction(void* out, const void* in, void* partials, int dtype, int op,
+                      const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
+                      int axis, long long output_len, const t4a_reduction_plan* plan,
+                      void* stream);
+
+/* 1 if t4a_hip_reduction runs `plan` over an input at `in` as one launch, else
+ * 0 (no reference counterpart: it tells a caller which kernels a profile will
+ * show). */
+int t4a_hip_reduction_joins(const void* in, int dtype, int op, const t4a_cuda_layout* out_layout,
+                            const t4a_cuda_layout* in_layout, int axis, long long output_len,
+                            const t4a_reduction_plan* plan);
+
 /* The hipError_t of the most recent launch on this thread that returned
  * T4A_HIP_ERR_LAUNCH (0 if none). */
 int t4a_hip_last_error(void);

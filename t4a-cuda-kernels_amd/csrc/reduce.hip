@@ -624,21 +624,91 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
   }
 }
 
+// One 32-lane plane's fold of its chunk (`len` elements from `chunk`; this
+// thread is lane `lane`), for the LEAN mapping below: all K 16-byte groups of
+// a lane loaded at once, non-temporally; the fold is the grouped walk's first
+// batch -- the first group seeds, the others join one at a time -- then the
+// tail element and the xor tree. A float Max / Min first folds in any order
+// with the IEEE maximum / minimum and takes the exact order only when the
+// plane's result is a NaN.
+template <typename T, int K>
+struct LeanShare {
+  Group<T, VecLanes<T>::value> b[K];
+  T t;  // the lane's tail element, if any
+};
+
+// Every load is unconditional -- a group past the chunk reloads group `lane`,
+// the tail of a lane without one reloads element 0 -- so no branch separates
+// them and all are in flight before the first wait; the fold skips the
+// stand-ins.
+template <typename T, int K>
+__device__ __forceinline__ void lean_load(LeanShare<T, K>& s, const T* chunk, int len, int lane) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int W = kWarp;
+  const int groups = len / V;
+  const int tail = groups * V;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int g = k == 0 || lane + k * W < groups ? lane + k * W : lane;
+    const Vec<T, V> x = nt_load<T, V>(chunk + g * V);
+    __builtin_memcpy(&s.b[k], &x, sizeof(s.b[k]));
+  }
+  // The tail (len mod V elements, lanes below it) is loaded only by planes
+  // whose chunk has one: usually none does.
+  s.t = s.b[0].x[0];
+  if (len != tail && lane < len - tail) s.t = chunk[tail + lane];
+}
+
+template <typename Fold, typename T, int K>
+__device__ __forceinline__ T lean_fold(const LeanShare<T, K>& s, int len, int lane, Fold f) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int W = kWarp;
+  const int groups = len / V;
+  const bool has_tail = lane < len - groups * V;
+  auto exact = [&]() {
+    T acc = group_value<Fold, T, V>(s.b[0], f);
+#pragma unroll
+    for (int k = 1; k < K; ++k) {
+      if (lane + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(s.b[k], f));
+    }
+    if (has_tail) acc = f.fold(acc, s.t);
+    return plane_tree(acc, W, f);
+  };
+  using Fast = typename AnyOrder<Fold, T>::type;
+  if constexpr (!std::is_void_v<Fast>) {
+    // Without a NaN any order gives the exact result. The stand-in loads
+    // repeat group `lane` and element 0 of the chunk (already among the lane's
+    // elements or the plane's), which an extremum ignores.
+    const Fast g;
+    T acc = s.t;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+      for (int c = 0; c < V; ++c) acc = g.combine(acc, s.b[k].x[c]);
+    }
+    const T reduced = plane_tree(acc, W, g);
+    return reduced != reduced ? exact() : reduced;
+  } else {
+    return exact();
+  }
+}
+
+template <typename Fold, typename T, int K>
+__device__ __forceinline__ T lean_chunk(const T* chunk, int len, int lane, Fold f) {
+  LeanShare<T, K> s;
+  lean_load(s, chunk, len, lane);
+  return lean_fold<Fold, T, K>(s, len, lane, f);
+}
+
 // LEAN plane mapping for a contiguous axis whose every chunk (the longer last
 // one included) holds at most K * 32 groups, so each lane's whole share is the
 // walk's first batch: one cube per 32-lane plane, consecutive planes on
-// consecutive cubes (consecutive memory on an inner axis), all K 16-byte groups
-// of a lane loaded at once, non-temporally. Few registers keep eight
-// wavefronts per SIMD in flight, which is what feeds HBM on this part; the
-// fold is the grouped walk's first batch -- the first group seeds, the others
-// join one at a time -- then the tail element and the xor tree. A float Max /
-// Min first folds in any order with the IEEE maximum / minimum and takes the
-// exact order only when the plane's result is a NaN.
+// consecutive cubes (consecutive memory on an inner axis). Few registers keep
+// eight wavefronts per SIMD in flight, which is what feeds HBM on this part.
 template <typename Fold, typename T, int K, bool Linear>
 __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in_ptr,
                                               const LeanPlan& lp, Fold f) {
   const unsigned int cubes = lp.cubes;
-  constexpr int V = VecLanes<T>::value;
   constexpr int W = kWarp;
   // The block size is the launcher's constant kBlock: reading blockDim would
   // cost every wavefront a memory round trip (it is an implicit kernel argument
@@ -690,54 +760,69 @@ __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in
       pidx = pb + static_cast<long long>(split) * lp.out_axis_stride;
       len = split + 1 == lp.splits.d ? lp.last_len : static_cast<int>(lp.chunk_len);
     }
-    const int groups = len / V;
-    const int tail = groups * V;
-    // Every load is unconditional -- a group past the chunk reloads group
-    // `lane`, the tail of a lane without one reloads element 0 -- so no branch
-    // separates them and all are in flight before the first wait; the folds
-    // below skip the stand-ins.
-    Group<T, V> b[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int g = k == 0 || lane + k * W < groups ? lane + k * W : lane;
-      const Vec<T, V> x = nt_load<T, V>(chunk + g * V);
-      __builtin_memcpy(&b[k], &x, sizeof(b[k]));
-    }
-    // The tail (len mod V elements, lanes below it) is loaded only by planes
-    // whose chunk has one: usually none does.
-    const bool has_tail = lane < len - tail;
-    T t = b[0].x[0];
-    if (len != tail && has_tail) t = chunk[tail + lane];
-    auto exact = [&]() {
-      T acc = group_value<Fold, T, V>(b[0], f);
-#pragma unroll
-      for (int k = 1; k < K; ++k) {
-        if (lane + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(b[k], f));
-      }
-      if (has_tail) acc = f.fold(acc, t);
-      return plane_tree(acc, W, f);
-    };
-    T reduced;
-    using Fast = typename AnyOrder<Fold, T>::type;
-    if constexpr (!std::is_void_v<Fast>) {
-      // Without a NaN any order gives the exact result; the tail element and
-      // unloaded groups repeat b[0].x[0], which an extremum ignores.
-      // The stand-in loads repeat group `lane` and element 0 of the chunk
-      // (already among the lane's elements or the plane's), which an extremum
-      // ignores.
-      const Fast g;
-      T acc = has_tail ? t : b[0].x[0];
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-#pragma unroll
-        for (int c = 0; c < V; ++c) acc = g.combine(acc, b[k].x[c]);
-      }
-      reduced = plane_tree(acc, W, g);
-      if (reduced != reduced) reduced = exact();
-    } else {
-      reduced = exact();
-    }
+    const T reduced = lean_chunk<Fold, T, K>(chunk, len, lane, f);
     if (lane == 0) partials[pidx] = reduced;
+  }
+}
+
+// Where a joined reduction writes its finals: output o at offset + o * stride
+// of `out`; each block holds `outputs` whole outputs (their splits' chunks).
+struct JoinedOut {
+  void* out;
+  long long offset;
+  long long stride;
+  unsigned int outputs;
+};
+
+// Pass 1 and the unit combine in one launch, for a linear LEAN plan of at most
+// 8 * C splits: a block's eight 32-lane planes fold the chunks of its outputs,
+// plane p the block's chunks p, p + 8, ... (up to C of them, every load issued
+// before the first fold), each chunk as partials_lean folds it, and write the
+// partials; then one thread per output folds that output's partials from LDS
+// serially from split 0, the reference's unit walk (reduce.cu:196-224) -- the
+// two launches' bits, with no memory traffic or ordering between blocks.
+template <typename Fold, typename CFold, typename T, int K, int C>
+__device__ __forceinline__ void reduction_joined(void* partials_ptr, const void* in_ptr,
+                                                 const LeanPlan& lp, const JoinedOut& jo,
+                                                 Fold f) {
+  constexpr int W = kWarp;
+  constexpr int kPlanes = kBlock / W;
+  __shared__ T joined[kPlanes * C];
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const int lane = threadIdx.x % W;
+  const unsigned int plane = threadIdx.x / W;
+  const unsigned int splits = lp.splits.d;
+  const unsigned int per_block = jo.outputs * splits;
+  // The launcher's grid holds no block without an output: `first` is a chunk.
+  const unsigned int first = blockIdx.x * per_block;
+  const int len = static_cast<int>(lp.chunk_len);
+  asm volatile("" ::"s"(lp.in_offset), "s"(lp.chunk_len), "s"(in));
+  LeanShare<T, K> s[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const unsigned int q = plane + c * kPlanes;
+    // A slot without a chunk reloads the block's first chunk (a stand-in).
+    const unsigned int cube = q < per_block && first + q < lp.cubes ? first + q : first;
+    lean_load(s[c], in + lp.in_offset + static_cast<long long>(cube) * lp.chunk_len, len, lane);
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const unsigned int q = plane + c * kPlanes;
+    const T reduced = lean_fold<Fold, T, K>(s[c], len, lane, f);
+    if (lane == 0 && q < per_block && first + q < lp.cubes) {
+      partials[lp.out_offset + static_cast<long long>(first + q) * lp.out_axis_stride] = reduced;
+      joined[q] = reduced;
+    }
+  }
+  __syncthreads();
+  const unsigned int o = blockIdx.x * jo.outputs + threadIdx.x;
+  if (threadIdx.x < jo.outputs && o * splits < lp.cubes) {
+    const T* p = joined + threadIdx.x * splits;
+    const CFold cf{};
+    T acc = cf.seed(p[0]);
+    for (unsigned int k = 1; k < splits; ++k) acc = cf.fold(acc, p[k]);
+    static_cast<T*>(jo.out)[jo.offset + static_cast<long long>(o) * jo.stride] = acc;
   }
 }
 
@@ -1188,6 +1273,15 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Pass 1 and the unit combine in one launch, up to C chunks per plane (linear
+// LEAN plans): CFold is the combine pass's fold (Sum after SumSquares, else the
+// same).
+template <typename T, int K, typename Fold, typename CFold, int C>
+__global__ void __launch_bounds__(kBlock)
+    reduction_joined_kernel(void* partials, const void* in, LeanPlan lp, JoinedOut jo) {
+  reduction_joined<Fold, CFold, T, K, C>(partials, in, lp, jo, Fold{});
+}
+
 // One kernel per (element type, batch slots, fold, linear walk): the fold is
 // chosen on the host, so each kernel carries one fold's code only.
 template <typename T, int K, typename Fold, bool Linear>
@@ -1526,4 +1620,173 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
     }
     return status_of_last_launch();
   });
+}
+
+// ---- a whole planned reduction ---------------------------------------------------
+
+namespace {
+
+template <typename T, int K, typename Fold, typename CFold, int C>
+void launch_joined_kernel(unsigned int grid, hipStream_t s, void* partials, const void* in,
+                          const t4a::LeanPlan& lp, const t4a::JoinedOut& jo) {
+  hipLaunchKernelGGL((t4a::reduction_joined_kernel<T, K, Fold, CFold, C>), dim3(grid),
+                     dim3(t4a::kBlock), 0, s, partials, in, lp, jo);
+}
+
+template <typename T, int K, typename Fold, typename CFold>
+void launch_joined_k(int c, unsigned int grid, hipStream_t s, void* partials, const void* in,
+                     const t4a::LeanPlan& lp, const t4a::JoinedOut& jo) {
+  switch (c) {
+    case 1: launch_joined_kernel<T, K, Fold, CFold, 1>(grid, s, partials, in, lp, jo); break;
+    case 2: launch_joined_kernel<T, K, Fold, CFold, 2>(grid, s, partials, in, lp, jo); break;
+    case 3: launch_joined_kernel<T, K, Fold, CFold, 3>(grid, s, partials, in, lp, jo); break;
+    default: launch_joined_kernel<T, K, Fold, CFold, 4>(grid, s, partials, in, lp, jo); break;
+  }
+}
+
+// How a Split plan runs joined (pass 1 and the combine in one launch): a unit
+// combine over at most 32 partials, the lean linear pass 1 (contiguous axis,
+// end-to-end equal chunks, 16-byte aligned input) and finals at offset +
+// o * stride, and at most eight 16-byte loads a lane once a block's eight
+// planes hold all of an output's chunks (heavier shares cost more than the
+// combine launch they save: i64 and f64 over 32 splits measured slower). Fills
+// the lean plan, the slot count, the chunks per plane, the grid and the
+// finals' place; false when the plan does not join.
+struct Joined {
+  t4a::LeanPlan lp;
+  t4a::JoinedOut jo;
+  int k;
+  int c;
+  unsigned int grid;
+};
+
+template <typename T, typename Fold, typename CFold>
+void launch_joined_fold(const Joined& j, hipStream_t s, void* partials, const void* in) {
+  switch (j.k) {
+    case 1: launch_joined_k<T, 1, Fold, CFold>(j.c, j.grid, s, partials, in, j.lp, j.jo);
+            break;
+    case 2: launch_joined_k<T, 2, Fold, CFold>(j.c, j.grid, s, partials, in, j.lp, j.jo);
+            break;
+    case 3: launch_joined_k<T, 3, Fold, CFold>(j.c, j.grid, s, partials, in, j.lp, j.jo);
+            break;
+    default:
+      launch_joined_k<T, 4, Fold, CFold>(j.c, j.grid, s, partials, in, j.lp, j.jo);
+      break;
+  }
+}
+
+bool joined_applies(const void* in, int dtype, int op, const t4a_cuda_layout& out_layout,
+                    const t4a_cuda_layout& in_layout, const t4a_cuda_layout& partials_layout,
+                    int axis, long long output_len, const t4a_reduction_plan& plan, Joined* j) {
+  const t4a_launch& l = plan.pass1;
+  const long long splits = plan.split.splits;
+  if (plan.kind != T4A_PLAN_SPLIT || plan.combine_strategy != T4A_CUDA_REDUCE_UNIT ||
+      splits < 1 || splits > t4a::kWarp || l.block[0] != static_cast<unsigned>(t4a::kBlock) ||
+      l.block[1] != 1 || l.block[2] != 1 || !t4a::sideways_dtype(dtype) || output_len < 1 ||
+      (reinterpret_cast<uintptr_t>(in) & 15) != 0)
+    return false;
+  t4a::PartialsPlan pp;
+  t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, t4a::kWarp, 1,
+                     t4a::dtype_size(dtype), 16);
+  if (pp.mode != t4a::kPartialsPlane) return false;
+  j->k = t4a::lean_slots(pp, dtype, op, splits, plan.split.chunk_len, t4a::kWarp);
+  if (j->k == 0) return false;
+  j->lp = t4a::lean_plan(pp, splits, plan.split.chunk_len);
+  if (!j->lp.linear) return false;
+  // The finals: output o at offset + o * stride (at most one fused dim, the
+  // partials' own).
+  t4a::ReduceDims ro;
+  t4a::reduce_dims(&ro, out_layout, in_layout, axis);
+  if (ro.n > 1 || ro.n != pp.dims.n || (ro.n == 1 && ro.ext[0] != pp.dims.ext[0])) return false;
+  j->jo.offset = ro.out_offset;
+  j->jo.stride = ro.n == 1 ? ro.os[0] : 0;
+  constexpr int kLoads = 8;
+  constexpr long long kPlanes = t4a::kBlock / t4a::kWarp;
+  j->c = static_cast<int>((splits + kPlanes - 1) / kPlanes);
+  if (j->c * j->k > kLoads) return false;
+  j->jo.outputs = static_cast<unsigned int>(kPlanes * j->c / splits);
+  j->grid = static_cast<unsigned int>((output_len + j->jo.outputs - 1) / j->jo.outputs);
+  return true;
+}
+
+// The joined launch when the plan allows it: returns -1 (no launch) otherwise.
+int try_joined(void* out, const void* in, void* partials, int dtype, int op,
+               const t4a_cuda_layout& out_layout, const t4a_cuda_layout& in_layout,
+               const t4a_cuda_layout& partials_layout, int axis, long long output_len,
+               const t4a_reduction_plan& plan, void* stream) {
+  Joined j;
+  if (!joined_applies(in, dtype, op, out_layout, in_layout, partials_layout, axis, output_len,
+                      plan, &j))
+    return -1;
+  j.jo.out = out;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return with_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (t4a::VecLanes<T>::value > 0) {
+      constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
+      switch (op) {
+        case T4A_CUDA_REDUCE_SUM:
+          launch_joined_fold<T, t4a::SumFold, t4a::SumFold>(j, s, partials, in);
+          break;
+        case T4A_CUDA_REDUCE_SUM_SQUARES:
+          if constexpr (kFloat)
+            launch_joined_fold<T, t4a::SumSquaresFold, t4a::SumFold>(j, s, partials, in);
+          break;
+        case T4A_CUDA_REDUCE_MAX:
+          launch_joined_fold<T, t4a::MaxFold, t4a::MaxFold>(j, s, partials, in);
+          break;
+        case T4A_CUDA_REDUCE_MIN:
+          launch_joined_fold<T, t4a::MinFold, t4a::MinFold>(j, s, partials, in);
+          break;
+        default: return -1;
+      }
+      return status_of_last_launch();
+    }
+    return -1;
+  });
+}
+
+}  // namespace
+
+extern "C" int t4a_hip_reduction(void* out, const void* in, void* partials, int dtype, int op,
+                                 const t4a_cuda_layout* out_layout,
+                                 const t4a_cuda_layout* in_layout, int axis, long long output_len,
+                                 const t4a_reduction_plan* plan, void* stream) {
+  if (plan == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (plan->kind == T4A_PLAN_DIRECT)
+    return t4a_hip_reduce(out, in, dtype, op, plan->strategy, out_layout, in_layout, axis,
+                          output_len, &plan->launch, stream);
+  t4a_cuda_layout pl;
+  if (int st = t4a_reduction_partials_layout(in_layout, static_cast<unsigned>(axis),
+                                             plan->split.splits, &pl))
+    return st;
+  if (launch_empty(&plan->pass1)) return T4A_OK;
+  if (out == nullptr || in == nullptr || partials == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const int joined = try_joined(out, in, partials, dtype, op, *out_layout, *in_layout, pl, axis,
+                                output_len, *plan, stream);
+  if (joined >= 0) return joined;
+  if (int st = t4a_hip_reduce_partials(partials, in, dtype, op, &pl, in_layout, axis, output_len,
+                                       plan->split.splits, plan->split.chunk_len, &plan->pass1,
+                                       stream))
+    return st;
+  return t4a_hip_reduce(out, partials, dtype, plan->combine_op, plan->combine_strategy,
+                        out_layout, &pl, axis, output_len, &plan->pass2, stream);
+}
+
+extern "C" int t4a_hip_reduction_joins(const void* in, int dtype, int op,
+                                       const t4a_cuda_layout* out_layout,
+                                       const t4a_cuda_layout* in_layout, int axis,
+                                       long long output_len, const t4a_reduction_plan* plan) {
+  if (plan == nullptr || out_layout == nullptr || in_layout == nullptr || in == nullptr ||
+      plan->kind != T4A_PLAN_SPLIT)
+    return 0;
+  t4a_cuda_layout pl;
+  if (t4a_reduction_partials_layout(in_layout, static_cast<unsigned>(axis), plan->split.splits,
+                                    &pl) != T4A_OK)
+    return 0;
+  Joined j;
+  return joined_applies(in, dtype, op, *out_layout, *in_layout, pl, axis, output_len, *plan, &j)
+             ? 1
+             : 0;
 }

@@ -301,6 +301,21 @@ class ReductionPlan:
     combine_op: Optional[ReduceOp] = None
     pass2: Optional[Launch] = None
 
+    def to_c(self) -> CReductionPlan:
+        c = CReductionPlan()
+        if self.kind == "Direct":
+            c.kind = 0
+            c.strategy = int(self.strategy)
+            c.launch = self.launch.to_c()
+        else:
+            c.kind = 1
+            c.split = self.split.to_c()
+            c.pass1 = self.pass1.to_c()
+            c.combine_strategy = int(self.combine_strategy)
+            c.combine_op = int(self.combine_op)
+            c.pass2 = self.pass2.to_c()
+        return c
+
 
 def _layout(x) -> CLayout:
     return x.c if isinstance(x, Layout) else x

@@ -115,6 +115,12 @@ SIGNATURES = {
     "t4a_hip_reduce_partials": (c_int, [c_void_p, c_void_p, c_int, c_int, POINTER(CLayout),
                                         POINTER(CLayout), c_int, c_longlong, c_longlong,
                                         c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_reduction": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                  POINTER(CLayout), POINTER(CLayout), c_int, c_longlong,
+                                  POINTER(CReductionPlan), c_void_p]),
+    "t4a_hip_reduction_joins": (c_int, [c_void_p, c_int, c_int, POINTER(CLayout),
+                                        POINTER(CLayout), c_int, c_longlong,
+                                        POINTER(CReductionPlan)]),
 }
 
 _LIB = None

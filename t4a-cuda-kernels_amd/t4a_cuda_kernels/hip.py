@@ -102,3 +102,24 @@ def enqueue_reduction(plan: ReductionPlan, out, inp, partials, dtype: DType, op:
     reduce(out, partials, dtype, plan.combine_op, plan.combine_strategy, out_layout,
            partials_layout, axis, output_len, plan.pass2, stream)
     return partials_layout
+
+
+def reduction(plan: ReductionPlan, out, inp, partials, dtype: DType, op: ReduceOp,
+              out_layout: Layout, in_layout: Layout, axis: int, output_len: int,
+              stream=None) -> None:
+    """A whole planned reduction through t4a_hip_reduction: one launch where
+    each block can hold all of an output's chunks (a unit combine over at most
+    32 partials of a contiguous axis), else pass 1 and the combine. `partials`
+    (the plan's partials layout) is written either way; None for Direct plans."""
+    _check(_lib.load().t4a_hip_reduction(
+        _ptr(out), _ptr(inp), _ptr(partials) if partials is not None else c_void_p(0),
+        int(dtype), int(op), byref(out_layout.c), byref(in_layout.c), axis, output_len,
+        byref(plan.to_c()), _stream(stream)))
+
+
+def reduction_joins(plan: ReductionPlan, inp, dtype: DType, op: ReduceOp, out_layout: Layout,
+                    in_layout: Layout, axis: int, output_len: int) -> bool:
+    """Whether `reduction` runs `plan` over `inp` as one launch."""
+    return bool(_lib.load().t4a_hip_reduction_joins(
+        _ptr(inp), int(dtype), int(op), byref(out_layout.c), byref(in_layout.c), axis,
+        output_len, byref(plan.to_c())))

@@ -314,3 +314,30 @@ def test_configuration_plans():
     plan = t.plan_reduction(DType.I32, ReduceOp.Prod, Layout.compact([1, 1048576, 32]),
                             1048576 * 32, inp, 4 * 1048576 * 32, 0, 32)
     assert plan.kind == "Direct" and plan.strategy == ReduceStrategy.Unit
+
+
+def test_reduction_joins_only_unit_combines_of_whole_chunks():
+    """Which Split plans t4a_hip_reduction runs as one launch (host logic only:
+    the input address is a number, nothing is dereferenced)."""
+    from t4a_cuda_kernels import hip
+    F32, I64 = t.DType.F32, t.DType.I64
+
+    def joins(dtype, n, rows, addr=0x10000, out_l=None, op=t.ReduceOp.Sum):
+        in_l = t.Layout.compact([n, rows])
+        out_l = out_l or t.Layout.compact([1, rows])
+        plan = t.plan_reduction(dtype, op, out_l, out_l.max_reachable_offset() + 1, in_l,
+                                n * rows, 0, 32)
+        assert plan.kind == "Split"
+        return hip.reduction_joins(plan, addr, dtype, op, out_l, in_l, 0, rows)
+
+    for n in (512, 1024, 1536, 3072, 4096, 6144, 8192):  # splits 2 .. 32, unit combines
+        assert joins(F32, n, 7)
+    for n in (512, 1024, 1536, 2048, 3072, 4096):  # splits 2 .. 16: at most 8 loads a lane
+        assert joins(I64, n, 3)
+    for n in (6144, 8192):  # 24 or 32 splits of 2 KiB chunks: 12 or 16 loads a lane
+        assert not joins(I64, n, 3)
+    assert joins(F32, 8192, 5, op=t.ReduceOp.Max)
+    assert joins(F32, 8192, 10, out_l=t.Layout([1, 10], [0, 3], 5))  # strided finals
+    assert not joins(F32, 8192, 7, addr=0x10004)  # input not 16-byte aligned
+    assert not joins(F32, 8960, 3)  # 35 splits: a plane combine
+    assert not joins(F32, 5000, 4)  # a longer last chunk
