@@ -48,10 +48,22 @@ struct TransposeShape {
 // each thread issues all of its loads before the first LDS write and all of its
 // LDS reads before the first store, with no edge tests; edge tiles and the
 // entry take the general loops.
-template <typename P, int VL, int VS, int BS>
+// The launcher's tile order: tiles of M and of N as precomputed divisors, the
+// tile count of one matrix (below 2^30, so every quotient input stays below
+// 2^31) and the grid's block count (gridDim.x costs two hidden-argument loads,
+// a scalar round trip after the alignment tests and before the first load).
+struct TileOrder {
+  FastDiv tiles_m;
+  FastDiv tiles_n;
+  unsigned int per_batch;
+  unsigned int blocks;
+};
+
+template <typename P, int VL, int VS, int BS, bool Ordered>
 __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __restrict__ src,
                                                 long long src_offset, long long S, long long M,
-                                                long long N, unsigned char* lds) {
+                                                long long N, const TileOrder& order,
+                                                unsigned char* lds) {
   constexpr int TM = TransposeShape<P>::TM;
   constexpr int TN = TransposeShape<P>::TN;
   constexpr int PITCH = TN + 1;
@@ -67,11 +79,9 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
   // and this build's 1-D one both cover every tile exactly once.
   const int tid = threadIdx.x + threadIdx.y * (BS > 0 ? BS : blockDim.x);
   const int nthreads = BS > 0 ? BS : blockDim.x * blockDim.y;
-  const long long nblocks = static_cast<long long>(gridDim.x) * gridDim.y;
-  for (long long t = blockIdx.x + static_cast<long long>(blockIdx.y) * gridDim.x;
-       t < per_batch; t += nblocks) {
-    const long long tm = t % tiles_m;
-    const long long tn = (t / tiles_m + tm) % tiles_n;
+  // Tile t of the matrix, in diagonal order: tm = t mod tiles_m, tn = (t div
+  // tiles_m + tm) mod tiles_n.
+  auto tile_body = [&](long long tm, long long tn) {
     const long long i0 = tm * TM;
     const long long j0 = tn * TN;
     const int rows = static_cast<int>(M - i0 < TM ? M - i0 : TM);
@@ -118,7 +128,7 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
           nt_store<P, VS>(d + (j0 + j) * M + i0 + i, y[r]);
         }
         __syncthreads();
-        continue;
+        return;
       }
     }
     // Source rows: runs of TN along j. VL divides N and src_offset, so a vector
@@ -145,14 +155,32 @@ __device__ __forceinline__ void transpose_tiles(P* __restrict__ dst, const P* __
       }
     }
     __syncthreads();
+  };
+  if constexpr (Ordered) {
+    // The launcher's 1-D grid over one matrix's tiles: 32-bit tile indices and
+    // precomputed divisors.
+    for (unsigned int t = blockIdx.x; t < order.per_batch; t += order.blocks) {
+      const unsigned int q = div_by(t, order.tiles_m);
+      const unsigned int tm = t - q * order.tiles_m.d;
+      const unsigned int u = q + tm;
+      tile_body(tm, u - div_by(u, order.tiles_n) * order.tiles_n.d);
+    }
+  } else {
+    const long long nblocks = static_cast<long long>(gridDim.x) * gridDim.y;
+    for (long long t = blockIdx.x + static_cast<long long>(blockIdx.y) * gridDim.x;
+         t < per_batch; t += nblocks) {
+      const long long tm = t % tiles_m;
+      tile_body(tm, (t / tiles_m + tm) % tiles_n);
+    }
   }
 }
 
-template <typename P, int BS>
+template <typename P, int BS, bool Ordered = false>
 __device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
                                                    long long src_offset, long long S,
                                                    long long M, long long N,
-                                                   unsigned char* lds) {
+                                                   unsigned char* lds,
+                                                   const TileOrder& order = TileOrder{}) {
   constexpr int V = sizeof(P) <= 8 ? 16 / static_cast<int>(sizeof(P)) : 1;
   const bool vl = V > 1 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && N % V == 0 &&
                   src_offset % V == 0;
@@ -160,13 +188,13 @@ __device__ __forceinline__ void transpose_dispatch(void* dst, const void* src,
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
   if (vl && vs) {
-    transpose_tiles<P, V, V, BS>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, V, V, BS, Ordered>(d, s, src_offset, S, M, N, order, lds);
   } else if (vl) {
-    transpose_tiles<P, V, 1, BS>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, V, 1, BS, Ordered>(d, s, src_offset, S, M, N, order, lds);
   } else if (vs) {
-    transpose_tiles<P, 1, V, BS>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, 1, V, BS, Ordered>(d, s, src_offset, S, M, N, order, lds);
   } else {
-    transpose_tiles<P, 1, 1, BS>(d, s, src_offset, S, M, N, lds);
+    transpose_tiles<P, 1, 1, BS, Ordered>(d, s, src_offset, S, M, N, order, lds);
   }
 }
 
@@ -490,68 +518,64 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
 // ---- copy_exact -----------------------------------------------------------------------
 // A bit-preserving copy of len elements (reference movement.cu:91-97, entry
 // 528-533). With both pointers 16-byte aligned the bytes stream as non-temporal
-// 16-byte vectors; the elements after the last whole vector, and unaligned
-// buffers, go element by element.
-constexpr int kCopyUnroll = 4;
-
+// 16-byte vectors, one per thread of the planned grid: on this part a copy
+// reaches HBM speed through many short-lived wavefronts with one load and one
+// store each (several vectors per thread measured 5-8 % slower, the extra
+// stores waiting behind each other). A smaller grid (the reference's geometry
+// through the module entry) strides over the rest. The elements after the last
+// whole vector, and unaligned buffers, go element by element.
 template <typename P, int BS>
 __device__ __forceinline__ void copy_elements(void* dst, const void* src, long long first,
-                                              long long len) {
+                                              long long len, unsigned int blocks) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
   const int bs = block_threads<BS>();
-  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  const long long gstride = static_cast<long long>(blocks) * bs;
   for (long long i = first + static_cast<long long>(blockIdx.x) * bs + threadIdx.x; i < len;
        i += gstride)
     d[i] = s[i];
 }
 
+// `blocks`: the grid's block count, an argument for the launcher's kernel
+// (gridDim.x costs hidden-argument loads, a second scalar round trip before
+// the first vector load), gridDim.x for the entry.
 template <typename P, int BS>
-__device__ __forceinline__ void copy_body(void* dst, const void* src, long long len) {
+__device__ __forceinline__ void copy_body(void* dst, const void* src, long long len,
+                                          unsigned int blocks) {
   const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) &
                         15) == 0;
   if (!aligned || sizeof(P) > 16) {
-    copy_elements<P, BS>(dst, src, 0, len);
+    copy_elements<P, BS>(dst, src, 0, len, blocks);
     return;
   }
-  // Each block streams one contiguous span of 16-byte vectors, its threads
-  // kCopyUnroll vectors apart per step, loads issued before stores.
-  using V16 = Vec<Bits128, 1>;
   const long long vectors = len * static_cast<long long>(sizeof(P)) / 16;
-  const long long span = (vectors + gridDim.x - 1) / gridDim.x;
-  const long long begin = static_cast<long long>(blockIdx.x) * span;
-  const long long end = begin + span < vectors ? begin + span : vectors;
   Bits128* d = static_cast<Bits128*>(dst);
   const Bits128* s = static_cast<const Bits128*>(src);
-  const long long step = block_threads<BS>();
-  long long i = begin + threadIdx.x;
-  for (; i + (kCopyUnroll - 1) * step < end; i += kCopyUnroll * step) {
-    V16 v[kCopyUnroll];
-#pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) v[u] = nt_load<Bits128, 1>(s + i + u * step);
-#pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) nt_store<Bits128, 1>(d + i + u * step, v[u]);
-  }
-  for (; i < end; i += step) nt_store<Bits128, 1>(d + i, nt_load<Bits128, 1>(s + i));
+  const int bs = block_threads<BS>();
+  for (long long i = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; i < vectors;
+       i += static_cast<long long>(blocks) * bs)
+    nt_store<Bits128, 1>(d + i, nt_load<Bits128, 1>(s + i));
   // Elements after the last whole vector.
-  copy_elements<P, BS>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len);
+  copy_elements<P, BS>(dst, src, vectors * 16 / static_cast<long long>(sizeof(P)), len,
+                       blocks);
 }
 
 // ---- kernels the launchers use: one per payload width, the plan computed on
 // the host and passed by value. ----
 
 template <typename P, int BS>
-__global__ void __launch_bounds__(256) copy_kernel(void* dst, const void* src, long long len) {
-  copy_body<P, BS>(dst, src, len);
+__global__ void __launch_bounds__(256)
+    copy_kernel(void* dst, const void* src, long long len, unsigned int blocks) {
+  copy_body<P, BS>(dst, src, len, blocks);
 }
 
-template <typename P, int BS>
+template <typename P, int BS, bool Ordered>
 __global__ void __launch_bounds__(512)
     transpose_kernel(void* dst, const void* src, long long src_offset, long long batch_stride,
-                     long long dst_fast_extent, long long src_fast_extent) {
+                     long long dst_fast_extent, long long src_fast_extent, TileOrder order) {
   __shared__ alignas(16) unsigned char lds[kTransposeLdsBytes];
-  transpose_dispatch<P, BS>(dst, src, src_offset, batch_stride, dst_fast_extent,
-                            src_fast_extent, lds);
+  transpose_dispatch<P, BS, Ordered>(dst, src, src_offset, batch_stride, dst_fast_extent,
+                                     src_fast_extent, lds, order);
 }
 
 template <typename P, int VL, int VS>
@@ -608,10 +632,10 @@ extern "C" __global__ void __launch_bounds__(512)
 extern "C" __global__ void __launch_bounds__(256)
     t4a_cuda_copy_exact(void* dst, const void* src, int dtype, long long len) {
   switch (t4a::dtype_size(dtype)) {
-    case 1: t4a::copy_body<uint8_t, 0>(dst, src, len); break;
-    case 4: t4a::copy_body<uint32_t, 0>(dst, src, len); break;
-    case 8: t4a::copy_body<unsigned long long, 0>(dst, src, len); break;
-    case 16: t4a::copy_body<t4a::Elem16, 0>(dst, src, len); break;
+    case 1: t4a::copy_body<uint8_t, 0>(dst, src, len, gridDim.x); break;
+    case 4: t4a::copy_body<uint32_t, 0>(dst, src, len, gridDim.x); break;
+    case 8: t4a::copy_body<unsigned long long, 0>(dst, src, len, gridDim.x); break;
+    case 16: t4a::copy_body<t4a::Elem16, 0>(dst, src, len, gridDim.x); break;
     default: break;
   }
 }
@@ -721,12 +745,32 @@ extern "C" int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype,
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kTransposeBlock))
-      hipLaunchKernelGGL((t4a::transpose_kernel<P, t4a::kTransposeBlock>), grid, block, 0, s, dst,
-                         src, src_offset, batch_stride, dst_fast_extent, src_fast_extent);
-    else
-      hipLaunchKernelGGL((t4a::transpose_kernel<P, 0>), grid, block, 0, s, dst, src, src_offset,
-                         batch_stride, dst_fast_extent, src_fast_extent);
+    // The planned geometry (one 1-D grid per matrix, 512 threads) takes the
+    // ordered kernel when one matrix has fewer than 2^30 tiles.
+    constexpr long long TM = t4a::TransposeShape<P>::TM;
+    constexpr long long TN = t4a::TransposeShape<P>::TN;
+    const long long tiles_m = (dst_fast_extent + TM - 1) / TM;
+    const long long tiles_n = (src_fast_extent + TN - 1) / TN;
+    t4a::TileOrder order{};
+    const bool planned =
+        block.x * block.y * block.z == static_cast<unsigned>(t4a::kTransposeBlock);
+    if (planned && grid.y == 1 && tiles_m > 0 && tiles_n > 0 &&
+        tiles_m * tiles_n < (1ll << 30)) {
+      order.tiles_m = t4a::fast_div(static_cast<unsigned int>(tiles_m));
+      order.tiles_n = t4a::fast_div(static_cast<unsigned int>(tiles_n));
+      order.per_batch = static_cast<unsigned int>(tiles_m * tiles_n);
+      order.blocks = grid.x;
+      hipLaunchKernelGGL((t4a::transpose_kernel<P, t4a::kTransposeBlock, true>), grid, block, 0,
+                         s, dst, src, src_offset, batch_stride, dst_fast_extent, src_fast_extent,
+                         order);
+    } else if (planned) {
+      hipLaunchKernelGGL((t4a::transpose_kernel<P, t4a::kTransposeBlock, false>), grid, block, 0,
+                         s, dst, src, src_offset, batch_stride, dst_fast_extent, src_fast_extent,
+                         order);
+    } else {
+      hipLaunchKernelGGL((t4a::transpose_kernel<P, 0, false>), grid, block, 0, s, dst, src,
+                         src_offset, batch_stride, dst_fast_extent, src_fast_extent, order);
+    }
     return status_of_last_launch();
   });
 }
@@ -742,9 +786,10 @@ extern "C" int t4a_hip_copy_exact(void* dst, const void* src, int dtype, long lo
     using P = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
-      hipLaunchKernelGGL((t4a::copy_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src, len);
+      hipLaunchKernelGGL((t4a::copy_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src, len,
+                         grid.x);
     else
-      hipLaunchKernelGGL((t4a::copy_kernel<P, 0>), grid, block, 0, s, dst, src, len);
+      hipLaunchKernelGGL((t4a::copy_kernel<P, 0>), grid, block, 0, s, dst, src, len, grid.x);
     return status_of_last_launch();
   });
 }

@@ -292,14 +292,14 @@ int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count) {
 }
 
 // Reference plan_copy_exact -> plan_elementwise (src/lib.rs:1592-1599, 1624-1626): every
-// dtype, flat_launch's refusals; each thread streams four 16-byte vectors.
+// dtype, flat_launch's refusals; each thread copies one 16-byte vector.
 int t4a_plan_copy_exact(int dtype, long long len, t4a_launch* launch) {
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
   if (int s = flat_launch_check(len)) return s;
   long long bytes;
   if (!checked_mul(len, t4a::dtype_size(dtype), &bytes)) return T4A_ERR_OVERFLOW;
-  set_launch(launch, len == 0 ? 0 : blocks_for(bytes, kBlock * 16 * 4), kBlock, 0);
+  set_launch(launch, len == 0 ? 0 : blocks_for(bytes, kBlock * 16), kBlock, 0);
   return ok();
 }
 

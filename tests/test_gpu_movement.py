@@ -13,7 +13,8 @@ import pytest
 
 import t4a_cuda_kernels as t
 from t4a_cuda_kernels import hip
-from gpu_util import (NUMPY, random_elements, say, sentinel, stream, to_device, to_host)
+from gpu_util import (NUMPY, SENTINEL, random_elements, say, sentinel, stream, to_device,
+                      to_host)
 from oracle import t4a_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -107,6 +108,40 @@ def test_tiled_transpose_full_size_round_trip():
     # dst[i + j*M] = src[i*N + j]: the first pass is the matrix transpose
     got = to_host(y, m * n * 4).view(np.int32).reshape(n, m)
     assert np.array_equal(got, host.reshape(m, n).T)
+
+
+@pytest.mark.parametrize("dtype", ALL_DTYPES, ids=[d.name for d in ALL_DTYPES])
+def test_copy_exact_aligned_shifted_and_tails(dtype):
+    """t4a_hip_copy_exact under its plan: 16-byte aligned buffers (whole vectors
+    plus a tail) and both pointers one element past a boundary (element path)."""
+    rng = np.random.default_rng(11)
+    for count in (1, 3, 17, 4096, 1_000_003):
+        src = random_elements(dtype, count + 4, rng)
+        d_src = to_device(src)
+        plan = t.plan_copy_exact(dtype, count)
+        for shift in (0, 1):
+            say("copy_exact", dtype.name, count, "shift", shift, "grid", plan.grid)
+            off = shift * dtype.size
+            d_dst = sentinel((count + 1) * dtype.size)
+            hip.copy_exact(d_dst.ptr + off, d_src.ptr + off, dtype, count, plan, stream())
+            got = to_host(d_dst, off + count * dtype.size)
+            assert (got[:off] == SENTINEL).all(), "a write landed before the destination"
+            want = np.ascontiguousarray(src[shift:shift + count]).view(np.uint8)
+            assert np.array_equal(got[off:], want), (dtype.name, count, shift)
+
+
+def test_copy_exact_full_size():
+    """256 MiB of f32 plus a three-element tail (the bench's copy, every vector
+    and the element path in one launch)."""
+    rng = np.random.default_rng(12)
+    count = (1 << 26) + 3
+    src = random_elements(t.DType.F32, count, rng)
+    plan = t.plan_copy_exact(t.DType.F32, count)
+    say("copy_exact full size", count, "grid", plan.grid)
+    d_src = to_device(src)
+    d_dst = sentinel(count * 4)
+    hip.copy_exact(d_dst, d_src, t.DType.F32, count, plan, stream())
+    assert np.array_equal(to_host(d_dst, count * 4), src.view(np.uint8))
 
 
 def run_materialize(dtype, layout, rng, src_len=None):
