@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "geometry.h"
 
@@ -216,11 +217,19 @@ struct AnyOrder {
   using type = void;
 };
 struct AnyOrderMax {
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const {
+    return ieee_maximum(a, v);
+  }
   template <typename T> __device__ __forceinline__ T combine(T a, T b) const {
     return ieee_maximum(a, b);
   }
 };
 struct AnyOrderMin {
+  template <typename T> __device__ __forceinline__ T seed(T v) const { return v; }
+  template <typename T> __device__ __forceinline__ T fold(T a, T v) const {
+    return ieee_minimum(a, v);
+  }
   template <typename T> __device__ __forceinline__ T combine(T a, T b) const {
     return ieee_minimum(a, b);
   }
@@ -229,6 +238,94 @@ template <> struct AnyOrder<MaxFold, float> { using type = AnyOrderMax; };
 template <> struct AnyOrder<MaxFold, double> { using type = AnyOrderMax; };
 template <> struct AnyOrder<MinFold, float> { using type = AnyOrderMin; };
 template <> struct AnyOrder<MinFold, double> { using type = AnyOrderMin; };
+
+// Folds whose combine is commutative bit for bit whenever the result is not a
+// NaN: real and integer additions (SUM, and SUM_SQUARES's combine), integer
+// extrema and the any-order float extrema. Their plane tree can pair lanes
+// with DPP moves instead of xor shuffles through LDS.
+template <typename Fold, typename T>
+struct Commutes {
+  static constexpr bool value = false;
+};
+template <typename T>
+constexpr bool kRealOrInt = std::is_same_v<T, float> || std::is_same_v<T, double> ||
+                            std::is_same_v<T, int> || std::is_same_v<T, long long>;
+template <typename T> struct Commutes<SumFold, T> { static constexpr bool value = kRealOrInt<T>; };
+template <typename T> struct Commutes<SumSquaresFold, T> {
+  static constexpr bool value = kRealOrInt<T>;
+};
+template <typename T> struct Commutes<MaxFold, T> {
+  static constexpr bool value = std::is_same_v<T, int> || std::is_same_v<T, long long>;
+};
+template <typename T> struct Commutes<MinFold, T> {
+  static constexpr bool value = std::is_same_v<T, int> || std::is_same_v<T, long long>;
+};
+template <typename T> struct Commutes<AnyOrderMax, T> {
+  static constexpr bool value = std::is_same_v<T, float> || std::is_same_v<T, double>;
+};
+template <typename T> struct Commutes<AnyOrderMin, T> {
+  static constexpr bool value = std::is_same_v<T, float> || std::is_same_v<T, double>;
+};
+
+// A DPP lane move of a 4- or 8-byte value (Ctrl: the DPP control word).
+template <int Ctrl, typename T>
+__device__ __forceinline__ T dpp_move(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "one or two words");
+  int w[sizeof(T) / 4];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (int k = 0; k < static_cast<int>(sizeof(T) / 4); ++k)
+    w[k] = __builtin_amdgcn_update_dpp(0, w[k], Ctrl, 0xF, 0xF, false);
+  __builtin_memcpy(&v, w, sizeof(T));
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+  int w[sizeof(T) / 4];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (int k = 0; k < static_cast<int>(sizeof(T) / 4); ++k)
+    w[k] = __builtin_amdgcn_readlane(w[k], lane);
+  __builtin_memcpy(&v, w, sizeof(T));
+  return v;
+}
+
+// The plane tree of a 32-lane plane (lanes 0-31 or 32-63 of the wavefront)
+// for a commuting fold; every lane of the plane ends with the result. The pairs
+// are the xor tree's: after offsets 1 and 2 (quad_perm moves) each quad holds
+// one value -- the two lanes of a pair compute combine(a, b) and combine(b,
+// a), equal for a commuting fold -- so row_half_mirror (lane i takes lane
+// 7 - i) pairs each quad with its xor-4 partner and, the eight lanes then
+// holding one value, row_mirror (i takes 15 - i) pairs each eight with its
+// xor-8 partner; offset 16 combines lanes 0 and 16 (or 32 and 48), read as
+// scalars. No LDS traffic and no waits, where an xor shuffle is an LDS permute
+// per offset. A float result that is a NaN (then so on every lane of the
+// plane) is recomputed by the own-left xor tree, whose NaN payload is the
+// reference's: commutativity holds only for non-NaN results. Every lane of the
+// plane must be active.
+template <typename Fold, typename T>
+__device__ __forceinline__ T plane_tree32(T v, Fold f) {
+  if constexpr (Commutes<Fold, T>::value) {
+    T r = f.combine(v, dpp_move<0xB1>(v));  // quad_perm [1, 0, 3, 2]: xor 1
+    r = f.combine(r, dpp_move<0x4E>(r));    // quad_perm [2, 3, 0, 1]: xor 2
+    r = f.combine(r, dpp_move<0x141>(r));   // row_half_mirror
+    r = f.combine(r, dpp_move<0x140>(r));   // row_mirror
+    // All four reads first: a read inside a conditional arm becomes a branch.
+    const T r0 = read_lane(r, 0);
+    const T r16 = read_lane(r, 16);
+    const T r32 = read_lane(r, 32);
+    const T r48 = read_lane(r, 48);
+    const bool upper = (threadIdx.x & 32) != 0;
+    r = f.combine(upper ? r32 : r0, upper ? r48 : r16);
+    if constexpr (std::is_same_v<T, float> || std::is_same_v<T, double>) {
+      if (r != r) r = plane_tree(v, kWarp, f);
+    }
+    return r;
+  } else {
+    return plane_tree(v, kWarp, f);
+  }
+}
 
 // Pairwise own-left tree over `n` register values (n a power of two); the
 // value of lane 0 of a plane whose lanes are held by one thread.

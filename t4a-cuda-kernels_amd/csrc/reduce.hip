@@ -634,14 +634,17 @@ __device__ __forceinline__ void partials_stream(void* partials_ptr, const void* 
 template <typename T, int K>
 struct LeanShare {
   Group<T, VecLanes<T>::value> b[K];
-  T t;  // the lane's tail element, if any
+  T t;  // the lane's tail element, if any (loaded with the groups)
 };
 
-// Every load is unconditional -- a group past the chunk reloads group `lane`,
-// the tail of a lane without one reloads element 0 -- so no branch separates
-// them and all are in flight before the first wait; the fold skips the
-// stand-ins.
-template <typename T, int K>
+// Every group load is unconditional -- a group past the chunk reloads group
+// `lane` -- so no branch separates them and all are in flight before the first
+// wait; the fold skips the stand-ins. The tail (len mod V elements, lanes below
+// it) is loaded here only by planes whose chunk has one, usually none. With
+// DeferTail the fold loads it instead: a plane holding several chunks would
+// otherwise wait for each chunk's first group (the tail's default) before
+// issuing the next chunk's loads.
+template <typename T, int K, bool DeferTail = false>
 __device__ __forceinline__ void lean_load(LeanShare<T, K>& s, const T* chunk, int len, int lane) {
   constexpr int V = VecLanes<T>::value;
   constexpr int W = kWarp;
@@ -653,18 +656,23 @@ __device__ __forceinline__ void lean_load(LeanShare<T, K>& s, const T* chunk, in
     const Vec<T, V> x = nt_load<T, V>(chunk + g * V);
     __builtin_memcpy(&s.b[k], &x, sizeof(s.b[k]));
   }
-  // The tail (len mod V elements, lanes below it) is loaded only by planes
-  // whose chunk has one: usually none does.
-  s.t = s.b[0].x[0];
-  if (len != tail && lane < len - tail) s.t = chunk[tail + lane];
+  if constexpr (!DeferTail) {
+    s.t = s.b[0].x[0];
+    if (len != tail && lane < len - tail) s.t = chunk[tail + lane];
+  }
 }
 
-template <typename Fold, typename T, int K>
-__device__ __forceinline__ T lean_fold(const LeanShare<T, K>& s, int len, int lane, Fold f) {
+template <typename Fold, typename T, int K, bool DeferTail = false>
+__device__ __forceinline__ T lean_fold(LeanShare<T, K>& s, const T* chunk, int len, int lane,
+                                       Fold f) {
   constexpr int V = VecLanes<T>::value;
   constexpr int W = kWarp;
   const int groups = len / V;
   const bool has_tail = lane < len - groups * V;
+  if constexpr (DeferTail) {
+    s.t = s.b[0].x[0];
+    if (has_tail) s.t = chunk[groups * V + lane];
+  }
   auto exact = [&]() {
     T acc = group_value<Fold, T, V>(s.b[0], f);
 #pragma unroll
@@ -672,7 +680,7 @@ __device__ __forceinline__ T lean_fold(const LeanShare<T, K>& s, int len, int la
       if (lane + k * W < groups) acc = f.combine(acc, group_value<Fold, T, V>(s.b[k], f));
     }
     if (has_tail) acc = f.fold(acc, s.t);
-    return plane_tree(acc, W, f);
+    return plane_tree32(acc, f);
   };
   using Fast = typename AnyOrder<Fold, T>::type;
   if constexpr (!std::is_void_v<Fast>) {
@@ -686,7 +694,7 @@ __device__ __forceinline__ T lean_fold(const LeanShare<T, K>& s, int len, int la
 #pragma unroll
       for (int c = 0; c < V; ++c) acc = g.combine(acc, s.b[k].x[c]);
     }
-    const T reduced = plane_tree(acc, W, g);
+    const T reduced = plane_tree32(acc, g);
     return reduced != reduced ? exact() : reduced;
   } else {
     return exact();
@@ -697,7 +705,7 @@ template <typename Fold, typename T, int K>
 __device__ __forceinline__ T lean_chunk(const T* chunk, int len, int lane, Fold f) {
   LeanShare<T, K> s;
   lean_load(s, chunk, len, lane);
-  return lean_fold<Fold, T, K>(s, len, lane, f);
+  return lean_fold<Fold, T, K>(s, chunk, len, lane, f);
 }
 
 // LEAN plane mapping for a contiguous axis whose every chunk (the longer last
@@ -804,12 +812,15 @@ __device__ __forceinline__ void reduction_joined(void* partials_ptr, const void*
     const unsigned int q = plane + c * kPlanes;
     // A slot without a chunk reloads the block's first chunk (a stand-in).
     const unsigned int cube = q < per_block && first + q < lp.cubes ? first + q : first;
-    lean_load(s[c], in + lp.in_offset + static_cast<long long>(cube) * lp.chunk_len, len, lane);
+    lean_load<T, K, true>(s[c], in + lp.in_offset + static_cast<long long>(cube) * lp.chunk_len,
+                          len, lane);
   }
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const unsigned int q = plane + c * kPlanes;
-    const T reduced = lean_fold<Fold, T, K>(s[c], len, lane, f);
+    const unsigned int cube = q < per_block && first + q < lp.cubes ? first + q : first;
+    const T reduced = lean_fold<Fold, T, K, true>(
+        s[c], in + lp.in_offset + static_cast<long long>(cube) * lp.chunk_len, len, lane, f);
     if (lane == 0 && q < per_block && first + q < lp.cubes) {
       partials[lp.out_offset + static_cast<long long>(first + q) * lp.out_axis_stride] = reduced;
       joined[q] = reduced;
@@ -974,7 +985,7 @@ __device__ __forceinline__ void side_unit(const SidePlan& sp, unsigned int u,
 // own-left xor tree.
 template <typename Fold, typename T, int CPL>
 __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* in_ptr,
-                                               const SidePlan& sp, Fold f, T* lds) {
+                                               const SidePlan& sp, Fold f, T* lds, int* redo) {
   constexpr int kWaves = kBlock / kWave;
   constexpr int kLanesPerWave = kWarp / kWaves;  // plane lanes per wavefront: 8
   constexpr int BC = kWave * CPL;                // columns per block
@@ -997,55 +1008,85 @@ __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* i
     const bool active = block_col + t * CPL < sp.columns;  // CPL divides the column count
     // the block's first column at row 0 of the split, uniform across the block
     const char* rows = in + (ib + block_col) * static_cast<long long>(sizeof(T));
-    T level[3][CPL];
-    T sub[CPL];
-    // Two plane lanes per step keep two lanes' loads in flight; the tree's
-    // climb is a uniform branch on the lane index.
+    // One pass of the unit under fold g: each wavefront's 8-lane subtree into
+    // LDS, then wavefront 0's columns meet as ((w0+w1)+(w2+w3)) in r.
+    auto pass = [&](auto g, T* r) {
+      T level[3][CPL];
+      T sub[CPL];
+      // Two plane lanes per step keep two lanes' loads in flight; the tree's
+      // climb is a uniform branch on the lane index.
 #pragma unroll 2
-    for (int a = 0; a < kLanesPerWave; ++a) {
-      T acc[CPL];
-      const int q0 = w * kLanesPerWave + a;
-      if (active) {
-        fold_lane_rows<CPL>(rows + q0 * row_bytes, kWarp * row_bytes, lane_off, q0, len, f,
-                            acc);
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] = T{};
-      }
-      // Binary counter: lane a's value climbs while a ends in ones.
-      if ((a & 1) == 0) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) level[0][c] = acc[c];
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] = f.combine(level[0][c], acc[c]);
-        if ((a & 2) == 0) {
-#pragma unroll
-          for (int c = 0; c < CPL; ++c) level[1][c] = acc[c];
+      for (int a = 0; a < kLanesPerWave; ++a) {
+        T acc[CPL];
+        const int q0 = w * kLanesPerWave + a;
+        if (active) {
+          fold_lane_rows<CPL>(rows + q0 * row_bytes, kWarp * row_bytes, lane_off, q0, len, g,
+                              acc);
         } else {
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = f.combine(level[1][c], acc[c]);
-          if ((a & 4) == 0) {
+          for (int c = 0; c < CPL; ++c) acc[c] = T{};
+        }
+        // Binary counter: lane a's value climbs while a ends in ones.
+        if ((a & 1) == 0) {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) level[2][c] = acc[c];
+          for (int c = 0; c < CPL; ++c) level[0][c] = acc[c];
+        } else {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) acc[c] = g.combine(level[0][c], acc[c]);
+          if ((a & 2) == 0) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) level[1][c] = acc[c];
           } else {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) sub[c] = f.combine(level[2][c], acc[c]);
+            for (int c = 0; c < CPL; ++c) acc[c] = g.combine(level[1][c], acc[c]);
+            if ((a & 4) == 0) {
+#pragma unroll
+              for (int c = 0; c < CPL; ++c) level[2][c] = acc[c];
+            } else {
+#pragma unroll
+              for (int c = 0; c < CPL; ++c) sub[c] = g.combine(level[2][c], acc[c]);
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) lds[w * BC + t * CPL + c] = sub[c];
-    __syncthreads();
+      for (int c = 0; c < CPL; ++c) lds[w * BC + t * CPL + c] = sub[c];
+      __syncthreads();
+      if (w == 0 && active) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int i = t * CPL + c;
+          r[c] = g.combine(g.combine(lds[i], lds[BC + i]),
+                           g.combine(lds[2 * BC + i], lds[3 * BC + i]));
+        }
+      }
+    };
+    T r[CPL];
+    using Fast = typename AnyOrder<Fold, T>::type;
+    if constexpr (!std::is_void_v<Fast> && sizeof(T) == 4) {
+      // An f32 Max / Min folds in any order with the IEEE maximum / minimum;
+      // when a column's result is a NaN the block redoes the unit in the
+      // exact order (wavefront 0 raises the flag, the whole block sees it).
+      // Not for f64: the second pass's registers cost the kernel occupancy.
+      pass(Fast{}, r);
+      bool nan = false;
+      if (w == 0 && active) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) nan = nan || r[c] != r[c];
+      }
+      if (threadIdx.x == 0) *redo = 0;
+      __syncthreads();
+      if (nan) *redo = 1;
+      __syncthreads();
+      if (*redo) {
+        pass(f, r);
+      }
+    } else {
+      pass(f, r);
+    }
     if (w == 0 && active) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int i = t * CPL + c;
-        const T r = f.combine(f.combine(lds[i], lds[BC + i]),
-                              f.combine(lds[2 * BC + i], lds[3 * BC + i]));
-        partials[pb + (block_col + i) * sp.col_os] = r;
-      }
+      for (int c = 0; c < CPL; ++c) partials[pb + (block_col + t * CPL + c) * sp.col_os] = r[c];
     }
     __syncthreads();  // the LDS tile is reused by the block's next unit
   }
@@ -1294,8 +1335,9 @@ template <typename T, int CPL>
 __global__ void __launch_bounds__(kBlock)
     partials_tiles_kernel(void* partials, const void* in, int op, SidePlan sp) {
   __shared__ T lds[(kBlock / kWave) * kWave * CPL];
+  __shared__ int redo;
   dispatch_fold<T>(op, [&](auto fold) {
-    partials_tiles<decltype(fold), T, CPL>(partials, in, sp, fold, lds);
+    partials_tiles<decltype(fold), T, CPL>(partials, in, sp, fold, lds, &redo);
   });
 }
 

@@ -289,6 +289,55 @@ def test_extrema_nan_payloads_bit_exact():
             assert list(zero_sign) == ([False, False] if op == Max else [True, True])
 
 
+def test_extrema_nan_payloads_outer_axis_bit_exact():
+    """The strided-axis pass 1 (one block per 128 columns of a split) folds f32
+    Max / Min in any order and redoes a unit in the exact order when one of its
+    columns comes out NaN: payloads in one column, two payloads in one column
+    (their order decides the result), a NaN in a split's last row, signed
+    zeros, infinities, every other column finite."""
+    rng = np.random.default_rng(12)
+    cols, n = 256, 8192
+    for dtype, bits, pl in ((F32, np.uint32, [0x7FC00001, 0x7F800001, 0xFFC00123, 0x7FFFFFFF]),
+                            (F64, np.uint64, [0x7FF8000000000001, 0x7FF0000000000001,
+                                              0xFFF8000000000123, 0x7FFFFFFFFFFFFFFF])):
+        for op in (Max, Min):
+            data = values(dtype, op, cols * n, rng)
+            raw = data.view(bits)
+            at = lambda c, r: r * cols + c                       # column c, row r
+            raw[at(3, 17)] = pl[0]
+            raw[at(130, 5)], raw[at(130, 4000)] = pl[2], pl[1]  # two in one column
+            raw[at(131, 4000)], raw[at(131, 5)] = pl[2], pl[1]  # the same, swapped rows
+            raw[at(200, 255)] = pl[3]                           # a split's last row
+            data[at(7, 0):at(7, n):cols] = -0.0                 # signed zeros only
+            data[at(7, 900)] = 0.0
+            data[at(8, 60)] = np.inf
+            data[at(9, 61)] = -np.inf
+            in_l = t.Layout.compact([cols, n])
+            out_l = t.Layout.compact([cols, 1])
+            plan = t.plan_reduction(dtype, op, out_l, cols, in_l, cols * n, 1, 32)
+            assert plan.kind == "Split"
+            say("outer extrema payloads", dtype.name, op.name, plan.split)
+            pl_l = t.reduction_partials_layout(in_l, 1, plan.split.splits)
+            pn = pl_l.element_count()
+            d_in, d_out, d_part = to_device(data), sentinel(cols * dtype.size), sentinel(
+                pn * dtype.size)
+            hip.enqueue_reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, 1, cols,
+                                  stream())
+            want_part = np.zeros(pn, dtype=NUMPY[dtype])
+            orc.reduce_partials(want_part, data, dtype, op, 32, pl_l, in_l, 1, cols,
+                                plan.split.splits, plan.split.chunk_len)
+            want = np.zeros(cols, dtype=NUMPY[dtype])
+            bw = plan.pass2.block[0] if plan.combine_strategy == t.ReduceStrategy.Plane else 32
+            orc.reduce(want, want_part, dtype, plan.combine_op, plan.combine_strategy, bw, out_l,
+                       pl_l, 1, cols)
+            got_part = to_host(d_part, pn * dtype.size, "partials")
+            got = to_host(d_out, cols * dtype.size, "output")
+            assert np.array_equal(got_part, want_part.view(np.uint8)), (dtype, op, "partials")
+            assert np.array_equal(got, want.view(np.uint8)), (dtype, op, "finals")
+            assert np.isnan(want[[3, 130, 131, 200]]).all()
+            assert np.signbit(want[7]) == (op == Min)
+
+
 def test_empty_output_is_no_launch():
     in_l = t.Layout.compact([5, 0])
     out_l = t.Layout.compact([1, 0])
