@@ -94,6 +94,38 @@ constexpr int kMaxDims = T4A_CUDA_MAX_RANK;
 constexpr long long kMoveRunMax = 128;
 constexpr long long kMoveTileBytes = 64 * 33 * 16;
 
+// Division of x < 2^31 by an invariant d >= 1 as a multiply-high, an add and a
+// shift (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, section 4): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, q = (mulhi(m, x) + x) >> l; x < 2^31 keeps
+// the sum inside 32 bits. AMD GPUs have no integer divide instruction: a
+// runtime 32-bit division is a dozen dependent instructions.
+struct FastDiv {
+  unsigned int d;
+  unsigned int m;
+  int shift;
+};
+
+T4A_HD FastDiv fast_div(unsigned int d) {
+  FastDiv f;
+  f.d = d;
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  f.shift = l;
+  f.m = static_cast<unsigned int>((((1ull << l) - d) << 32) / d + 1);
+  return f;
+}
+
+T4A_HD unsigned int div_by(unsigned int x, const FastDiv& f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned int t = __umulhi(f.m, x);
+#else
+  const unsigned int t =
+      static_cast<unsigned int>((static_cast<unsigned long long>(f.m) * x) >> 32);
+#endif
+  return (t + x) >> f.shift;
+}
+
 struct MovePlan {
   int mode;
   int n;                      // fused dims
@@ -118,6 +150,10 @@ struct MovePlan {
   int batch_dims[kMaxDims];
   long long a_tiles, b_tiles;
   long long tiles;            // total work items (tiles, rows or elements)
+  // Tile coordinates as 32-bit quotients when tiles < 2^30: the divisors of
+  // the coordinate extents in walk order (A tiles, B tiles, batch dims).
+  bool coords32;
+  FastDiv coord_div[kMaxDims + 2];
   // CONTIG: dim `row_dim` is contiguous on both sides; rows are decoded over
   // the other dims.
   int row_dim;
@@ -136,6 +172,7 @@ T4A_HD int move_chain_contains(const int* dims, int count, int dim) {
 T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* dst_strides,
                       long long dst_offset, long long len, int esize) {
   p->mode = kMoveEmpty;
+  p->coords32 = false;
   p->n = 0;
   p->len = len;
   p->src_offset = src.offset;
@@ -189,15 +226,16 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
     p->tiles = len;
     return;
   }
-  // Tile budget: 4096 elements up to 8 bytes (<= 32 KiB of LDS), 2048 for
-  // 16-byte elements; each run aims for 64 elements (32 for 16-byte elements
-  // on the source side). A run whose chain ends short leaves its share of the
-  // budget to the other run, up to kMoveRunMax elements (a power of two), as
-  // long as the padded tile fits kMoveTileBytes: a 32-element source run
-  // then feeds 128-element destination runs.
-  const long long budget = esize >= 16 ? 2048 : 4096;
-  long long target_a = 64;
-  long long target_b = esize >= 16 ? 32 : 64;
+  // Tile budget: 16 KiB of elements -- 4096 of 4 bytes or less (runs aiming
+  // for 64 x 64), 2048 of 8 bytes (64 x 32), 1024 of 16 bytes (32 x 32): a
+  // tile per block with more blocks per CU measured faster than larger tiles.
+  // A run whose chain ends short leaves its share of the budget to the other
+  // run, up to kMoveRunMax elements (a power of two), as long as the padded
+  // tile fits kMoveTileBytes: a 16-element source run then feeds 128-element
+  // destination runs.
+  const long long budget = esize >= 16 ? 1024 : esize >= 8 ? 2048 : 4096;
+  long long target_a = esize >= 16 ? 32 : 64;
+  long long target_b = esize >= 8 ? 32 : 64;
   p->a_dims[0] = a;
   p->na = 1;
   p->b_dims[0] = b;
@@ -296,6 +334,86 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
   }
   p->mode = kMoveTiled;
   p->tiles = tiles;
+  p->coords32 = tiles < (1ll << 30);
+  if (p->coords32) {
+    p->coord_div[0] = fast_div(static_cast<unsigned int>(p->a_tiles));
+    p->coord_div[1] = fast_div(static_cast<unsigned int>(p->b_tiles));
+    for (int q = 0; q < p->nbatch; ++q)
+      p->coord_div[q + 2] = fast_div(static_cast<unsigned int>(p->ext[p->batch_dims[q]]));
+  }
+}
+
+// The one-tile-per-block form of a TILED plan: a block moves tile blockIdx.x
+// whole, all of a thread's loads issued before its first LDS write, the tile
+// shape a compile-time LA x LB. It applies when each chain has at most two
+// dims (an inner one at full extent, the tiled outer one), the tile count is
+// below 2^30 (32-bit coordinates) and (la, lb) is one of the shapes below.
+struct TilePlan {
+  long long src_offset, dst_offset;
+  long long a_ss0, a_ss1;  // source strides of the A chain's inner and outer dims
+  long long b_ds0, b_ds1;  // destination strides of the B chain's inner and outer dims
+  FastDiv a_in, b_in;      // the inner dims' extents (1 for a one-dim chain)
+  unsigned int a_tile, b_tile;  // tile extents along the outer dims
+  unsigned int a_last, b_last;  // the outer dims' extents
+  int ncoord;                   // coordinates of the tile walk: A tile, B tile, batch dims
+  int skew_first, skew_second;  // diagonal order (see the persistent walk), -1 if none
+  FastDiv coord[kMaxDims + 2];
+  long long coord_ss[kMaxDims + 2];  // source / destination offset per unit of a coordinate
+  long long coord_ds[kMaxDims + 2];
+};
+
+// Compile-time tile shapes, the planner's full tiles when both chains reach
+// their targets: 64 x 64 for 4-byte elements, 64 x 32 for 8-byte ones and
+// 32 x 32 for 16-byte ones.
+T4A_HD bool tile_once_shape(long long la, long long lb, int esize) {
+  if (esize == 4) return la == 64 && lb == 64;
+  if (esize == 8) return la == 64 && lb == 32;
+  if (esize == 16) return la == 32 && lb == 32;
+  return false;
+}
+
+T4A_HD bool tile_plan(TilePlan* tp, const MovePlan& p, int esize) {
+  if (p.mode != kMoveTiled || !p.coords32 || p.na > 2 || p.nb > 2 ||
+      !tile_once_shape(p.la, p.lb, esize))
+    return false;
+  tp->src_offset = p.src_offset;
+  tp->dst_offset = p.dst_offset;
+  const int a_outer = p.a_dims[p.na - 1];
+  const int b_outer = p.b_dims[p.nb - 1];
+  tp->a_in = fast_div(p.na == 2 ? static_cast<unsigned int>(p.ext[p.a_dims[0]]) : 1u);
+  tp->a_ss0 = p.na == 2 ? p.ss[p.a_dims[0]] : 0;
+  tp->a_ss1 = p.ss[a_outer];
+  tp->b_in = fast_div(p.nb == 2 ? static_cast<unsigned int>(p.ext[p.b_dims[0]]) : 1u);
+  tp->b_ds0 = p.nb == 2 ? p.ds[p.b_dims[0]] : 0;
+  tp->b_ds1 = p.ds[b_outer];
+  tp->a_tile = static_cast<unsigned int>(p.a_tile);
+  tp->b_tile = static_cast<unsigned int>(p.b_tile);
+  tp->a_last = static_cast<unsigned int>(p.ext[a_outer]);
+  tp->b_last = static_cast<unsigned int>(p.ext[b_outer]);
+  tp->ncoord = 2 + p.nbatch;
+  long long ext[kMaxDims + 2];
+  ext[0] = p.a_tiles;
+  ext[1] = p.b_tiles;
+  tp->coord_ss[0] = p.a_tile * p.ss[a_outer];
+  tp->coord_ds[0] = p.a_tile * p.ds[a_outer];
+  tp->coord_ss[1] = p.b_tile * p.ss[b_outer];
+  tp->coord_ds[1] = p.b_tile * p.ds[b_outer];
+  for (int q = 0; q < p.nbatch; ++q) {
+    const int k = p.batch_dims[q];
+    ext[q + 2] = p.ext[k];
+    tp->coord_ss[q + 2] = p.ss[k];
+    tp->coord_ds[q + 2] = p.ds[k];
+  }
+  // Diagonal order only between the A and B tile coordinates (a transpose's
+  // tiles): skewing one batch dim by another scatters the writes of blocks
+  // that run together, which measured slower.
+  tp->skew_first = tp->skew_second = -1;
+  if (ext[0] > 1 && ext[1] > 1) {
+    tp->skew_first = 0;
+    tp->skew_second = 1;
+  }
+  for (int q = 0; q < tp->ncoord; ++q) tp->coord[q] = p.coord_div[q];
+  return true;
 }
 
 // ---- reductions ---------------------------------------------------------------
@@ -355,37 +473,6 @@ T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
   }
 }
 
-// Division of x < 2^31 by an invariant d >= 1 as a multiply-high, an add and a
-// shift (Granlund and Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994, section 4): with l = ceil(log2 d) and
-// m = floor(2^32 (2^l - d) / d) + 1, q = (mulhi(m, x) + x) >> l; x < 2^31 keeps
-// the sum inside 32 bits. AMD GPUs have no integer divide instruction: a
-// runtime 32-bit division is a dozen dependent instructions.
-struct FastDiv {
-  unsigned int d;
-  unsigned int m;
-  int shift;
-};
-
-T4A_HD FastDiv fast_div(unsigned int d) {
-  FastDiv f;
-  f.d = d;
-  int l = 0;
-  while ((1ull << l) < d) ++l;
-  f.shift = l;
-  f.m = static_cast<unsigned int>((((1ull << l) - d) << 32) / d + 1);
-  return f;
-}
-
-T4A_HD unsigned int div_by(unsigned int x, const FastDiv& f) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const unsigned int t = __umulhi(f.m, x);
-#else
-  const unsigned int t =
-      static_cast<unsigned int>((static_cast<unsigned long long>(f.m) * x) >> 32);
-#endif
-  return (t + x) >> f.shift;
-}
 
 // The unit kernels' compact plan: at most three fused output dims with
 // precomputed divisors, 32-bit output indices. `vector`: the axis is contiguous

@@ -229,24 +229,42 @@ __device__ __forceinline__ TileCoords tile_coords(const MovePlan& p, long long t
   long long rest = t;
   long long first = 0;
   int seen = 0;
-  auto coord = [&](long long extent) {
-    long long c = rest % extent;
-    rest /= extent;
+  // Coordinate q of the walk (extent `extent`): 32-bit quotients by the plan's
+  // precomputed divisors when the tile count is below 2^30 (every rest, and a
+  // coordinate plus the first one, then stays below 2^31), else 64-bit ones.
+  auto coord = [&](int q, long long extent) {
+    long long c;
+    if (p.coords32) {
+      const unsigned int r = static_cast<unsigned int>(rest);
+      const unsigned int quot = div_by(r, p.coord_div[q]);
+      c = r - quot * p.coord_div[q].d;
+      rest = quot;
+    } else {
+      c = rest % extent;
+      rest /= extent;
+    }
     if (extent > 1) {
-      if (seen == 1) c = (c + first) % extent;
+      if (seen == 1) {
+        if (p.coords32) {
+          const unsigned int u = static_cast<unsigned int>(c + first);
+          c = u - div_by(u, p.coord_div[q]) * p.coord_div[q].d;
+        } else {
+          c = (c + first) % extent;
+        }
+      }
       if (seen == 0) first = c;
       ++seen;
     }
     return c;
   };
-  const long long ta = coord(p.a_tiles);
-  const long long tb = coord(p.b_tiles);
+  const long long ta = coord(0, p.a_tiles);
+  const long long tb = coord(1, p.b_tiles);
   TileCoords tc;
   tc.sbase = p.src_offset + ta * p.a_tile * p.ss[a_last] + tb * p.b_tile * p.ss[b_last];
   tc.dbase = p.dst_offset + ta * p.a_tile * p.ds[a_last] + tb * p.b_tile * p.ds[b_last];
   for (int q = 0; q < p.nbatch; ++q) {
     const int k = p.batch_dims[q];
-    const long long c = coord(p.ext[k]);
+    const long long c = coord(q + 2, p.ext[k]);
     tc.sbase += c * p.ss[k];
     tc.dbase += c * p.ds[k];
   }
@@ -262,7 +280,7 @@ __device__ __forceinline__ TileCoords tile_coords(const MovePlan& p, long long t
 constexpr int kTileThreads = 256;
 template <typename P>
 constexpr int max_tile_elems() {
-  return sizeof(P) >= 16 ? 64 * 32 : 64 * 64;
+  return sizeof(P) >= 16 ? 32 * 32 : sizeof(P) >= 8 ? 64 * 32 : 64 * 64;
 }
 
 template <typename P, int VL, int VS>
@@ -350,6 +368,95 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
     if (next >= p.tiles) break;
     t = next;
     cur = nxt;
+  }
+}
+
+// One tile per block (TilePlan): the tile's coordinates from blockIdx.x by
+// precomputed divisors (uniform, scalar), then every load of the thread
+// issued before its first LDS write, as in the tiled transpose; element (i, j)
+// of the LA x LB tile sits at src_base + src_a(i) + j and dst_base + i +
+// dst_b(j), the chain offsets decoded per slot (at most two digits). A partial
+// tile's empty slots load the tile's first element instead (so no branch
+// separates the loads) and are neither parked nor stored.
+template <typename P, int VL, int VS, int LA, int LB>
+__device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __restrict__ src,
+                                               const TilePlan& tp, P* tile) {
+  constexpr int BS = kBlock;
+  constexpr int PITCH = LB + 1;
+  constexpr int LBV = LB / VL;
+  constexpr int LAV = LA / VS;
+  constexpr int RL = LA * LBV / BS;
+  constexpr int RS = LB * LAV / BS;
+  static_assert(RL * BS == LA * LBV && RS * BS == LB * LAV, "the block divides the tile");
+  unsigned int rest = blockIdx.x;
+  unsigned int first = 0, ta = 0, tb = 0;
+  long long sb = tp.src_offset;
+  long long db = tp.dst_offset;
+#pragma unroll
+  for (int q = 0; q < kMaxDims + 2; ++q) {
+    if (q < tp.ncoord) {
+      const unsigned int quot = div_by(rest, tp.coord[q]);
+      unsigned int c = rest - quot * tp.coord[q].d;
+      rest = quot;
+      if (q == tp.skew_second) {
+        const unsigned int u = c + first;
+        c = u - div_by(u, tp.coord[q]) * tp.coord[q].d;
+      }
+      if (q == tp.skew_first) first = c;
+      if (q == 0) ta = c;
+      if (q == 1) tb = c;
+      sb += static_cast<long long>(c) * tp.coord_ss[q];
+      db += static_cast<long long>(c) * tp.coord_ds[q];
+    }
+  }
+  const unsigned int a_left = tp.a_last - ta * tp.a_tile;
+  const unsigned int b_left = tp.b_last - tb * tp.b_tile;
+  const int va = static_cast<int>(tp.a_in.d * (a_left < tp.a_tile ? a_left : tp.a_tile));
+  const int vb = static_cast<int>(tp.b_in.d * (b_left < tp.b_tile ? b_left : tp.b_tile));
+  const P* s = src + sb;
+  P* d = dst + db;
+  const int tid = threadIdx.x;
+  auto src_a = [&](int i) {
+    const unsigned int o = div_by(static_cast<unsigned int>(i), tp.a_in);
+    return static_cast<long long>(i - static_cast<int>(o * tp.a_in.d)) * tp.a_ss0 +
+           static_cast<long long>(o) * tp.a_ss1;
+  };
+  auto dst_b = [&](int j) {
+    const unsigned int o = div_by(static_cast<unsigned int>(j), tp.b_in);
+    return static_cast<long long>(j - static_cast<int>(o * tp.b_in.d)) * tp.b_ds0 +
+           static_cast<long long>(o) * tp.b_ds1;
+  };
+  Vec<P, VL> x[RL];
+#pragma unroll
+  for (int r = 0; r < RL; ++r) {
+    const int e = tid + r * BS;
+    const int i = e / LBV;
+    const int j = (e % LBV) * VL;
+    const bool valid = i < va && j < vb;
+    x[r] = nt_load<P, VL>(valid ? s + src_a(i) + j : s);
+  }
+#pragma unroll
+  for (int r = 0; r < RL; ++r) {
+    const int e = tid + r * BS;
+    const int i = e / LBV;
+    const int j = (e % LBV) * VL;
+    if (i < va && j < vb) {
+#pragma unroll
+      for (int k = 0; k < VL; ++k) tile[i * PITCH + j + k] = x[r].v[k];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int e = tid + r * BS;
+    const int j = e / LAV;
+    const int i = (e % LAV) * VS;
+    if (i < va && j < vb) {
+      Vec<P, VS> y;
+#pragma unroll
+      for (int k = 0; k < VS; ++k) y.v[k] = tile[(i + k) * PITCH + j];
+      nt_store<P, VS>(d + i + dst_b(j), y);
+    }
   }
 }
 
@@ -585,6 +692,13 @@ __global__ void __launch_bounds__(256)
   move_tiled_as<P, VL, VS>(dst, src, plan, lds);
 }
 
+template <typename P, int VL, int VS, int LA, int LB>
+__global__ void __launch_bounds__(kBlock)
+    move_tile_once_kernel(void* dst, const void* src, TilePlan tp) {
+  __shared__ P tile[LA * (LB + 1)];
+  move_tile_once<P, VL, VS, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src), tp, tile);
+}
+
 template <typename P, int BS>
 __global__ void __launch_bounds__(256) move_flat_kernel(void* dst, const void* src, MovePlan plan) {
   if (plan.mode == kMoveContig) {
@@ -696,6 +810,27 @@ bool config_valid(const t4a_cuda_transpose_config& c) {
          T4A_OK;
 }
 
+template <typename P, int VL, int VS>
+void launch_tile_shape(dim3 grid, hipStream_t s, void* dst, const void* src,
+                       const t4a::TilePlan& tp) {
+  constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
+  constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
+  hipLaunchKernelGGL((t4a::move_tile_once_kernel<P, VL, VS, LA, LB>), grid, dim3(t4a::kBlock), 0,
+                     s, dst, src, tp);
+}
+
+// The one-tile kernels by vector widths (t4a::tile_once_shape's shapes).
+template <typename P, int V>
+void launch_tile_once(bool vl, bool vs, dim3 grid, hipStream_t s, void* dst, const void* src,
+                      const t4a::TilePlan& tp) {
+  if constexpr (V > 1) {
+    if (vl && vs) return launch_tile_shape<P, V, V>(grid, s, dst, src, tp);
+    if (vl) return launch_tile_shape<P, V, 1>(grid, s, dst, src, tp);
+    if (vs) return launch_tile_shape<P, 1, V>(grid, s, dst, src, tp);
+  }
+  launch_tile_shape<P, 1, 1>(grid, s, dst, src, tp);
+}
+
 int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
                 const t4a_launch* launch, void* stream, int dtype) {
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
@@ -714,6 +849,15 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
     constexpr int V = t4a::tile_vector<P>();
     bool vl, vs;
     t4a::tile_vectorizable(plan, V, dst, src, &vl, &vs);
+    if constexpr (sizeof(P) >= 4) {
+      t4a::TilePlan tp;
+      if (block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 && block.z == 1 &&
+          grid.y == 1 && grid.z == 1 && static_cast<long long>(grid.x) == plan.tiles &&
+          t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P)))) {
+        launch_tile_once<P, V>(vl, vs, grid, s, dst, src, tp);
+        return status_of_last_launch();
+      }
+    }
     if (vl && vs) {
       hipLaunchKernelGGL((t4a::move_tiled_kernel<P, V, V>), grid, block, 0, s, dst, src, plan);
     } else if (vl) {

@@ -135,12 +135,17 @@ int flat_launch_check(long long len) {
   return ok();
 }
 
-void movement_launch(const t4a::MovePlan& plan, t4a_launch* out) {
+void movement_launch(const t4a::MovePlan& plan, int esize, t4a_launch* out) {
   long long blocks = 0;
+  t4a::TilePlan tp;
   switch (plan.mode) {
-    // Tiled blocks are persistent: four per CU on 256 CUs, each pipelining its
+    // A tile shape of the one-tile kernels: one block per tile. Otherwise
+    // tiled blocks are persistent: four per CU on 256 CUs, each pipelining its
     // run of tiles (the next tile's loads overlap the current tile's stores).
-    case t4a::kMoveTiled: blocks = plan.tiles < 1024 ? plan.tiles : 1024; break;
+    case t4a::kMoveTiled:
+      blocks = t4a::tile_plan(&tp, plan, esize) ? plan.tiles
+                                                  : (plan.tiles < 1024 ? plan.tiles : 1024);
+      break;
     case t4a::kMoveContig: blocks = blocks_for(plan.len, kBlock * 4); break;
     case t4a::kMoveGeneric: blocks = blocks_for(plan.len, kBlock * 4); break;
     default: blocks = 0; break;
@@ -316,7 +321,7 @@ int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long lon
   if (int s = flat_launch_check(len)) return s;
   t4a::MovePlan plan;
   t4a::move_plan(&plan, *src, nullptr, 0, len, es);
-  movement_launch(plan, launch);
+  movement_launch(plan, es, launch);
   return ok();
 }
 
@@ -340,7 +345,7 @@ int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long
   if (int s = flat_launch_check(len)) return s;
   t4a::MovePlan plan;
   t4a::move_plan(&plan, *src, dst->strides, dst->offset, len, es);
-  movement_launch(plan, launch);
+  movement_launch(plan, es, launch);
   return ok();
 }
 

@@ -49,8 +49,9 @@ int main() {
     ++checked;
     if (p.mode != kMoveTiled) continue;
     ++tiled;
-    const long long budget = es >= 16 ? 2048 : 4096;
-    const long long max_elems = es >= 16 ? 64 * 32 : 64 * 64;  // register stage of move_tiles
+    const long long budget = es >= 16 ? 1024 : es >= 8 ? 2048 : 4096;
+    // register stage of move_tiles
+    const long long max_elems = es >= 16 ? 32 * 32 : es >= 8 ? 64 * 32 : 64 * 64;
     bool ok = p.la >= 1 && p.lb >= 1 && p.la <= kMoveRunMax && p.lb <= kMoveRunMax &&
               p.la * p.lb <= budget && p.la * p.lb <= max_elems &&
               p.la * (p.lb + 1) * es <= kMoveTileBytes;
