@@ -53,14 +53,14 @@ ROTATE = 3
 # and the factor is that over what the counter reports for it. A kernel change
 # needs a new measurement; until then the entry is left out and traffic is null.
 TRAFFIC: dict[tuple[str, str], dict] = {
-    ("c2", "sum_i64_inner"): {"bytes": 538906757, "source": "profiles/traffic_c2_sum_i64_inner.md"},
-    ("c2", "sum_f32_inner"): {"bytes": 269755725, "source": "profiles/traffic_c2_sum_f32_inner.md"},
-    ("c2", "sum_f32_outer"): {"bytes": 269531508, "source": "profiles/traffic_c2_sum_f32_outer.md"},
-    ("c1big", "transpose_f32_8192"): {"bytes": 537115975, "source": "profiles/traffic_c1big_transpose_f32_8192.md"},
-    ("c3", "permute4_F64"): {"bytes": 268721201, "source": "profiles/traffic_c3_permute4_F64.md"},
-    ("c4", "sumsq_f32_middle"): {"bytes": 538974472, "source": "profiles/traffic_c4_sumsq_f32_middle.md"},
-    ("c4", "prod_i32_last"): {"bytes": 671205919, "source": "profiles/traffic_c4_prod_i32_last.md"},
-    ("c5", "permute6_c64"): {"bytes": 537114280, "source": "profiles/traffic_c5_permute6_c64.md"},
+    ("c2", "sum_i64_inner"): {"bytes": 538948628, "source": "profiles/traffic_c2_sum_i64_inner.md"},
+    ("c2", "sum_f32_inner"): {"bytes": 269794476, "source": "profiles/traffic_c2_sum_f32_inner.md"},
+    ("c2", "sum_f32_outer"): {"bytes": 269562792, "source": "profiles/traffic_c2_sum_f32_outer.md"},
+    ("c1big", "transpose_f32_8192"): {"bytes": 536952925, "source": "profiles/traffic_c1big_transpose_f32_8192.md"},
+    ("c3", "permute4_F64"): {"bytes": 268455680, "source": "profiles/traffic_c3_permute4_F64.md"},
+    ("c4", "sumsq_f32_middle"): {"bytes": 539009101, "source": "profiles/traffic_c4_sumsq_f32_middle.md"},
+    ("c4", "prod_i32_last"): {"bytes": 671012891, "source": "profiles/traffic_c4_prod_i32_last.md"},
+    ("c5", "permute6_c64"): {"bytes": 537005613, "source": "profiles/traffic_c5_permute6_c64.md"},
 }
 
 NUMPY_DTYPE = {t.DType.F32: np.float32, t.DType.F64: np.float64, t.DType.I32: np.int32,
