@@ -7,6 +7,7 @@
  * against the reference passes byte-identical arguments:
  *
  *   t4a_cuda_layout            reference cuda/include/t4a/abi.cuh:47-57
+ *   t4a_cuda_layout_any        reference cuda/include/t4a/abi.cuh:109-121
  *   t4a_cuda_transpose_config  reference cuda/include/t4a/abi.cuh:239-245
  *   t4a_cuda_dtype tags        reference cuda/include/t4a/abi.cuh:25-33
  *   reduce op / strategy tags  reference cuda/include/t4a/abi.cuh:59-71
@@ -61,6 +62,20 @@ typedef struct {
   long long strides[T4A_CUDA_MAX_RANK];
 } t4a_cuda_layout;
 
+/* The general-rank layout of the `_any` entries (reference revision 9,
+ * docs/abi/c-kernel-abi.md "Dynamic rank"): the same fields with `rank` values
+ * of extents and of strides in caller-owned device memory (8-byte aligned,
+ * unchanged until the launch completes; may be NULL when rank is 0). 32 bytes,
+ * alignment 8: rank 0, reserved 4, offset 8, extents 16, strides 24. The
+ * t4a_plan_*_any planners take the same struct pointing at host memory. */
+typedef struct {
+  int rank;
+  int reserved;
+  long long offset;
+  const long long* extents;
+  const long long* strides;
+} t4a_cuda_layout_any;
+
 typedef enum {
   T4A_CUDA_REDUCE_SUM = 0,
   T4A_CUDA_REDUCE_PROD = 1,
@@ -99,6 +114,12 @@ T4A_STATIC_ASSERT(T4A_ALIGNOF(t4a_cuda_layout) == 8, "t4a_cuda_layout alignment"
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout, offset) == 8, "t4a_cuda_layout.offset");
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout, extents) == 16, "t4a_cuda_layout.extents");
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout, strides) == 80, "t4a_cuda_layout.strides");
+T4A_STATIC_ASSERT(sizeof(void*) == 8, "the C ABI requires 64-bit pointers");
+T4A_STATIC_ASSERT(sizeof(t4a_cuda_layout_any) == 32, "t4a_cuda_layout_any size");
+T4A_STATIC_ASSERT(T4A_ALIGNOF(t4a_cuda_layout_any) == 8, "t4a_cuda_layout_any alignment");
+T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, offset) == 8, "t4a_cuda_layout_any.offset");
+T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, extents) == 16, "t4a_cuda_layout_any.extents");
+T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, strides) == 24, "t4a_cuda_layout_any.strides");
 T4A_STATIC_ASSERT(sizeof(t4a_cuda_transpose_config) == 16, "t4a_cuda_transpose_config size");
 T4A_STATIC_ASSERT(T4A_ALIGNOF(t4a_cuda_transpose_config) == 4,
                   "t4a_cuda_transpose_config alignment");

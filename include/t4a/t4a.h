@@ -20,8 +20,11 @@
  *
  * Status values: 0 is success; otherwise the reference `Error` discriminant
  * plus one (reference src/lib.rs:217-274), or one of the T4A_HIP_* launch
- * statuses below. Rank is bounded by T4A_CUDA_MAX_RANK (the reference's fast
- * path, `Layout`/`CLayout`).
+ * statuses below. The by-value planners and launchers take rank <= 8
+ * (T4A_CUDA_MAX_RANK, the reference's fast path `Layout`/`CLayout`); their
+ * `_any` twins take t4a_cuda_layout_any of any rank (the reference's general
+ * path, docs/abi/c-kernel-abi.md "Dynamic rank"): the planners read its arrays
+ * from host memory, the launchers pass arrays in device memory to the kernels.
  */
 #ifndef T4A_T4A_H_
 #define T4A_T4A_H_
@@ -156,6 +159,36 @@ int t4a_plan_reduction(int dtype, int op, const t4a_cuda_layout* out_layout, lon
 int t4a_reduction_partials_layout(const t4a_cuda_layout* in_layout, unsigned int axis,
                                   long long splits, t4a_cuda_layout* partials_layout);
 
+/* ---- general-rank planners ------------------------------------------------------
+ * The same validation, errors and geometry for layouts of any rank (reference
+ * planners over LayoutRef / WideLayout, whose rank is not bounded), with the
+ * layouts' arrays in HOST memory. `launch->variant` is T4A_VARIANT_GENERAL when
+ * a rank exceeds 8 (reference RankVariant::select, src/lib.rs:817-838): launch
+ * the `_any` twin then; at rank <= 8 either twin runs the geometry. */
+int t4a_plan_materialize_strided_any(int dtype, const t4a_cuda_layout_any* src,
+                                     long long src_len, t4a_launch* launch);
+int t4a_plan_strided_to_strided_any(int dtype, const t4a_cuda_layout_any* src,
+                                    long long src_len, const t4a_cuda_layout_any* dst,
+                                    long long dst_len, t4a_launch* launch);
+int t4a_plan_reduce_any(int dtype, int op, int strategy, const t4a_cuda_layout_any* out_layout,
+                        long long out_len, const t4a_cuda_layout_any* in_layout,
+                        long long in_len, unsigned int axis, unsigned int plane_width,
+                        t4a_launch* launch);
+int t4a_plan_reduce_partials_any(int dtype, int op, const t4a_cuda_layout_any* partials_layout,
+                                 long long partials_len, const t4a_cuda_layout_any* in_layout,
+                                 long long in_len, unsigned int axis, t4a_split split,
+                                 unsigned int plane_width, t4a_launch* launch);
+/* Writes pass1 / pass2 variants as above. */
+int t4a_plan_reduction_any(int dtype, int op, const t4a_cuda_layout_any* out_layout,
+                           long long out_len, const t4a_cuda_layout_any* in_layout,
+                           long long in_len, unsigned int axis, unsigned int plane_width,
+                           t4a_reduction_plan* plan);
+/* The compact partials layout of any rank: `in_layout->rank` extents and
+ * strides into the caller's arrays (offset 0). */
+int t4a_reduction_partials_layout_any(const t4a_cuda_layout_any* in_layout, unsigned int axis,
+                                      long long splits, long long* extents,
+                                      long long* strides);
+
 /* ---- HIP launchers ------------------------------------------------------------
  * Each launches the gfx950 kernel of the reference entry's name with the
  * arguments of that entry, on `stream` (a hipStream_t; NULL is the null stream),
@@ -191,6 +224,28 @@ int t4a_hip_reduce_partials(void* partials, const void* in, int dtype, int op,
                             const t4a_cuda_layout* in_layout, int axis, long long output_len,
                             long long splits, long long chunk_len, const t4a_launch* launch,
                             void* stream);
+
+/* The general-rank twins (reference cuda/src/movement.cu:620-646,
+ * cuda/src/reduce.cu:854-940): the layouts' arrays in device memory, ordered
+ * before the launch on `stream` and unchanged until it completes; any geometry
+ * from the matching t4a_plan_*_any (or by-value) planner. The kernels fuse the
+ * geometry themselves and return the by-value twins' bits. */
+int t4a_hip_materialize_strided_any(void* dst, const void* src, int dtype,
+                                    const t4a_cuda_layout_any* src_layout, long long len,
+                                    const t4a_launch* launch, void* stream);
+int t4a_hip_strided_to_strided_any(void* dst, const void* src, int dtype,
+                                   const t4a_cuda_layout_any* src_layout,
+                                   const t4a_cuda_layout_any* dst_layout, long long len,
+                                   const t4a_launch* launch, void* stream);
+int t4a_hip_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
+                       const t4a_cuda_layout_any* out_layout,
+                       const t4a_cuda_layout_any* in_layout, int axis, long long output_len,
+                       const t4a_launch* launch, void* stream);
+int t4a_hip_reduce_partials_any(void* partials, const void* in, int dtype, int op,
+                                const t4a_cuda_layout_any* partials_layout,
+                                const t4a_cuda_layout_any* in_layout, int axis,
+                                long long output_len, long long splits, long long chunk_len,
+                                const t4a_launch* launch, void* stream);
 
 /* A whole reduction_plan (reference src/lib.rs:3457-3528 plans it; its caller
  * then launches pass 1 and the combine, reduce.cu:813-852 and 765-811): Direct

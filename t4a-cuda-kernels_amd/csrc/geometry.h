@@ -168,26 +168,60 @@ T4A_HD int move_chain_contains(const int* dims, int count, int dim) {
   return 0;
 }
 
+// Fused movement geometry of any rank: every axis of extent 1 dropped, and an
+// axis whose source and destination strides both continue the previous kept
+// axis's span merged into it (axis 0 first). `ds == nullptr` means the compact
+// destination of materialize_strided (strides by the running extent product).
+// Writes at most `cap` fused axes to fe / fs / fd and returns their count, or
+// -1 when more remain. With no extent 0 every fused axis has extent >= 2, so a
+// layout of fewer than 2^63 elements fuses to at most 62 axes.
+constexpr int kMaxFusedDims = 64;
+
+T4A_HD int fuse_move(int rank, const long long* ext, const long long* ss, const long long* ds,
+                     long long* fe, long long* fs, long long* fd, int cap) {
+  int n = 0;
+  unsigned long long compact = 1;
+  for (int k = 0; k < rank; ++k) {
+    const long long e = ext[k];
+    const long long s = ss[k];
+    const long long d = ds ? ds[k] : static_cast<long long>(compact);
+    compact *= static_cast<unsigned long long>(e);
+    if (e == 1) continue;
+    if (n > 0 && s == fs[n - 1] * fe[n - 1] && d == fd[n - 1] * fe[n - 1]) {
+      fe[n - 1] *= e;
+      continue;
+    }
+    if (n == cap) return -1;
+    fe[n] = e;
+    fs[n] = s;
+    fd[n] = d;
+    ++n;
+  }
+  return n;
+}
+
 // `dst_strides == nullptr` means the compact destination of materialize_strided.
-T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* dst_strides,
-                      long long dst_offset, long long len, int esize) {
+// The source is `rank` axes of extents `src_ext` and strides `src_str` (at most
+// kMaxDims are read) from `src_offset`.
+T4A_HD void move_plan_view(MovePlan* p, int rank, long long src_offset, const long long* src_ext,
+                           const long long* src_str, const long long* dst_strides,
+                           long long dst_offset, long long len, int esize) {
   p->mode = kMoveEmpty;
   p->coords32 = false;
   p->n = 0;
   p->len = len;
-  p->src_offset = src.offset;
+  p->src_offset = src_offset;
   p->dst_offset = dst_offset;
   p->na = p->nb = p->nbatch = 0;
   p->tiles = 0;
   p->row_dim = -1;
   if (len <= 0) return;
-  int rank = src.rank;
   if (rank < 0) rank = 0;
   if (rank > kMaxDims) rank = kMaxDims;
   long long compact = 1;
   for (int k = 0; k < rank; ++k) {
-    const long long e = src.extents[k];
-    const long long s = src.strides[k];
+    const long long e = src_ext[k];
+    const long long s = src_str[k];
     const long long d = dst_strides ? dst_strides[k] : compact;
     compact *= e;
     if (e == 1) continue;
@@ -343,6 +377,12 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
   }
 }
 
+T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* dst_strides,
+                      long long dst_offset, long long len, int esize) {
+  move_plan_view(p, src.rank, src.offset, src.extents, src.strides, dst_strides, dst_offset, len,
+                 esize);
+}
+
 // The one-tile-per-block form of a TILED plan: a block moves tile blockIdx.x
 // whole, all of a thread's loads issued before its first LDS write, the tile
 // shape a compile-time LA x LB. It applies when each chain has at most two
@@ -422,11 +462,16 @@ T4A_HD bool tile_plan(TilePlan* tp, const MovePlan& p, int esize) {
 // neighbours merged where both the input and the output (or partials) strides
 // continue each other. The output index decodes over them in axis order, as
 // reduce.cu:110-130 decodes it over the output layout.
-struct ReduceDims {
+// The fused non-axis dims of a reduction, at most N of them: ReduceDims (N =
+// kMaxDims) for the by-value entries and plans, ReduceDimsWide for the
+// general-rank `_any` entries, built in LDS.
+template <int N>
+struct ReduceDimsN {
+  static constexpr int kDims = N;
   int n;
-  long long ext[kMaxDims];
-  long long is[kMaxDims];  // input strides
-  long long os[kMaxDims];  // output / partials strides
+  long long ext[N];
+  long long is[N];  // input strides
+  long long os[N];  // output / partials strides
   long long in_offset;
   long long out_offset;
   long long axis_len;
@@ -434,29 +479,43 @@ struct ReduceDims {
   long long out_axis_stride;  // partials stride of the split coordinate
   bool narrow;                // the product of ext[] is below 2^32
 };
+using ReduceDims = ReduceDimsN<kMaxDims>;
+using ReduceDimsWide = ReduceDimsN<kMaxFusedDims>;
 
-T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
-                        const t4a_cuda_layout& in, int axis) {
+// Fuse the non-axis dims of a reduction of any rank (extent-1 dims dropped,
+// a dim merged into the previous kept one when its input and output strides
+// both continue that one's span; the axis is skipped, so dims on its two sides
+// may merge) into r. `out_ext` gives the non-axis extents; the axis takes its
+// length and stride from the input and its output stride (the partials' split
+// stride, or the keepdims output's) from the output. False, with r->n = -1,
+// when more than N dims remain.
+template <int N>
+T4A_HD bool reduce_dims_view(ReduceDimsN<N>* r, int rank, int axis, long long out_offset,
+                             const long long* out_ext, const long long* out_str,
+                             long long in_offset, const long long* in_ext,
+                             const long long* in_str) {
   r->n = 0;
-  r->in_offset = in.offset;
-  r->out_offset = out.offset;
-  r->axis_len = in.extents[axis];
-  r->axis_stride = in.strides[axis];
-  r->out_axis_stride = out.strides[axis];
-  int rank = out.rank;
-  if (rank > kMaxDims) rank = kMaxDims;
+  r->in_offset = in_offset;
+  r->out_offset = out_offset;
+  r->axis_len = in_ext[axis];
+  r->axis_stride = in_str[axis];
+  r->out_axis_stride = out_str[axis];
   for (int k = 0; k < rank; ++k) {
     if (k == axis) continue;
-    const long long e = out.extents[k];
+    const long long e = out_ext[k];
     if (e == 1) continue;
-    const long long s = in.strides[k];
-    const long long o = out.strides[k];
+    const long long s = in_str[k];
+    const long long o = out_str[k];
     if (r->n > 0) {
       const int last = r->n - 1;
       if (s == r->is[last] * r->ext[last] && o == r->os[last] * r->ext[last]) {
         r->ext[last] *= e;
         continue;
       }
+    }
+    if (r->n == N) {
+      r->n = -1;
+      return false;
     }
     r->ext[r->n] = e;
     r->is[r->n] = s;
@@ -471,6 +530,15 @@ T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
     total *= e;
     if (total > 0xffffffffull) r->narrow = false;
   }
+  return true;
+}
+
+T4A_HD void reduce_dims(ReduceDims* r, const t4a_cuda_layout& out,
+                        const t4a_cuda_layout& in, int axis) {
+  int rank = out.rank;
+  if (rank > kMaxDims) rank = kMaxDims;
+  reduce_dims_view(r, rank, axis, out.offset, out.extents, out.strides, in.offset, in.extents,
+                   in.strides);
 }
 
 

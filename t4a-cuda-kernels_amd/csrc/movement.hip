@@ -622,6 +622,76 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
   }
 }
 
+// General-rank movement (reference movement.cu:620-646, docs/abi/c-kernel-abi.md
+// "Dynamic rank"): the geometry arrays live in caller-owned device memory.
+// Thread 0 fuses them into LDS (extent-1 axes dropped, chained axes merged);
+// at most kMaxDims fused axes take the by-value entries' plan and mappings,
+// more (at most 62: each has extent >= 2) a per-element decode over the fused
+// axes, axis 0 first, as the reference decodes.
+template <typename P>
+__device__ __forceinline__ void move_elements_wide(void* dst, const void* src, int n,
+                                                   const long long* fe, const long long* fs,
+                                                   const long long* fd, long long src_offset,
+                                                   long long dst_offset, long long len) {
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < len;
+       f += gstride) {
+    long long rest = f;
+    long long so = src_offset;
+    long long dof = dst_offset;
+    for (int k = 0; k < n; ++k) {
+      const long long c = rest % fe[k];
+      rest /= fe[k];
+      so += c * fs[k];
+      dof += c * fd[k];
+    }
+    d[dof] = s[so];
+  }
+}
+
+// `dst_layout == nullptr`: the compact destination of materialize_strided.
+// Ranks that differ, or a negative rank, do no work.
+__device__ __forceinline__ void move_entry_any(void* dst, const void* src, int dtype,
+                                               const t4a_cuda_layout_any& src_layout,
+                                               const t4a_cuda_layout_any* dst_layout,
+                                               long long len) {
+  const int es = dtype_size(dtype);
+  if (es == 0 || len <= 0) return;
+  __shared__ MovePlan plan;
+  __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
+  __shared__ int fused;
+  __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
+  const long long dst_offset = dst_layout ? dst_layout->offset : 0;
+  if (threadIdx.x == 0) {
+    fused = -1;
+    if (src_layout.rank >= 0 && (dst_layout == nullptr || dst_layout->rank == src_layout.rank)) {
+      fused = fuse_move(src_layout.rank, src_layout.extents, src_layout.strides,
+                        dst_layout ? dst_layout->strides : nullptr, fe, fs, fd, kMaxFusedDims);
+      if (fused >= 0 && fused <= kMaxDims)
+        move_plan_view(&plan, fused, src_layout.offset, fe, fs, fd, dst_offset, len, es);
+    }
+  }
+  __syncthreads();
+  if (fused < 0) return;
+  auto run = [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    if (fused <= kMaxDims) {
+      move_dispatch<P>(dst, src, plan, lds);
+    } else {
+      move_elements_wide<P>(dst, src, fused, fe, fs, fd, src_layout.offset, dst_offset, len);
+    }
+  };
+  switch (es) {
+    case 1: run(static_cast<uint8_t*>(nullptr)); break;
+    case 4: run(static_cast<uint32_t*>(nullptr)); break;
+    case 8: run(static_cast<unsigned long long*>(nullptr)); break;
+    case 16: run(static_cast<Elem16*>(nullptr)); break;
+    default: break;
+  }
+}
+
 // ---- copy_exact -----------------------------------------------------------------------
 // A bit-preserving copy of len elements (reference movement.cu:91-97, entry
 // 528-533). With both pointers 16-byte aligned the bytes stream as non-temporal
@@ -766,6 +836,19 @@ extern "C" __global__ void __launch_bounds__(256)
                                 long long len) {
   // Both layouts share the source's extents (reference movement.cu:139-141).
   t4a::move_entry(dst, src, dtype, src_layout, dst_layout.strides, dst_layout.offset, len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_materialize_strided_any(void* dst, const void* src, int dtype,
+                                     t4a_cuda_layout_any src_layout, long long len) {
+  t4a::move_entry_any(dst, src, dtype, src_layout, nullptr, len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_strided_to_strided_any(void* dst, const void* src, int dtype,
+                                    t4a_cuda_layout_any src_layout,
+                                    t4a_cuda_layout_any dst_layout, long long len) {
+  t4a::move_entry_any(dst, src, dtype, src_layout, &dst_layout, len);
 }
 
 // ---- launchers -----------------------------------------------------------------------
@@ -961,4 +1044,37 @@ extern "C" int t4a_hip_strided_to_strided(void* dst, const void* src, int dtype,
   t4a::move_plan(&plan, *src_layout, dst_layout->strides, dst_layout->offset, len,
                  t4a::dtype_size(dtype));
   return launch_move(dst, src, plan, launch, stream, dtype);
+}
+
+// The general-rank twins on the caller's stream with a planned geometry (any
+// t4a_plan_*_any geometry: the twins stride over their work).
+extern "C" int t4a_hip_materialize_strided_any(void* dst, const void* src, int dtype,
+                                               const t4a_cuda_layout_any* src_layout,
+                                               long long len, const t4a_launch* launch,
+                                               void* stream) {
+  if (launch == nullptr || src_layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  hipLaunchKernelGGL(t4a_cuda_materialize_strided_any, grid, block, 0,
+                     static_cast<hipStream_t>(stream), dst, src, dtype, *src_layout, len);
+  return status_of_last_launch();
+}
+
+extern "C" int t4a_hip_strided_to_strided_any(void* dst, const void* src, int dtype,
+                                              const t4a_cuda_layout_any* src_layout,
+                                              const t4a_cuda_layout_any* dst_layout,
+                                              long long len, const t4a_launch* launch,
+                                              void* stream) {
+  if (launch == nullptr || src_layout == nullptr || dst_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  hipLaunchKernelGGL(t4a_cuda_strided_to_strided_any, grid, block, 0,
+                     static_cast<hipStream_t>(stream), dst, src, dtype, *src_layout, *dst_layout,
+                     len);
+  return status_of_last_launch();
 }

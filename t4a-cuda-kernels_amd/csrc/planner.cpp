@@ -10,6 +10,7 @@
 #include <climits>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 
 #include "geometry.h"
 #include "t4a/t4a.h"
@@ -40,32 +41,60 @@ bool checked_add(long long a, long long b, long long* out) {
   return !__builtin_add_overflow(a, b, out);
 }
 
-// Reference LayoutRef::new / Layout::new validation (src/lib.rs:342-360, 908-928).
-int check_layout(const t4a_cuda_layout* l) {
-  if (l == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
-  if (l->rank < 0 || l->rank > T4A_CUDA_MAX_RANK) return T4A_ERR_RANK_OUT_OF_RANGE;
-  for (int k = 0; k < l->rank; ++k) {
-    if (l->extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
+// A layout as the planners read it, of any rank: the by-value t4a_cuda_layout
+// (rank <= 8) or the general-rank t4a_cuda_layout_any pointing at host memory
+// (the reference planners take LayoutRef slices of any rank).
+struct View {
+  int rank;
+  long long offset;
+  const long long* extents;
+  const long long* strides;
+};
+
+View V(const t4a_cuda_layout* l) { return View{l->rank, l->offset, l->extents, l->strides}; }
+View V(const t4a_cuda_layout_any* l) {
+  return View{l->rank, l->offset, l->extents, l->strides};
+}
+
+// Reference LayoutRef::new / Layout::new validation (src/lib.rs:342-360, 908-928):
+// rank at most `max_rank` (8 for the by-value layout, unbounded for the
+// general-rank one, reference WideLayout), no negative extent.
+int check_view(const View& l, int max_rank) {
+  if (l.rank < 0 || l.rank > max_rank) return T4A_ERR_RANK_OUT_OF_RANGE;
+  if (l.rank > 0 && (l.extents == nullptr || l.strides == nullptr))
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  for (int k = 0; k < l.rank; ++k) {
+    if (l.extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
   }
   return T4A_OK;
 }
 
+int check_layout(const t4a_cuda_layout* l) {
+  if (l == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  return check_view(V(l), T4A_CUDA_MAX_RANK);
+}
+
+int check_any(const t4a_cuda_layout_any* l) {
+  if (l == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  return check_view(V(l), INT_MAX);
+}
+
 // Reference element_count (src/lib.rs:392-397).
-int element_count(const t4a_cuda_layout* l, long long* count) {
+int element_count(const View& l, long long* count) {
   long long acc = 1;
-  for (int k = 0; k < l->rank; ++k) {
-    if (!checked_mul(acc, l->extents[k], &acc)) return T4A_ERR_OVERFLOW;
+  for (int k = 0; k < l.rank; ++k) {
+    if (!checked_mul(acc, l.extents[k], &acc)) return T4A_ERR_OVERFLOW;
   }
   *count = acc;
   return T4A_OK;
 }
 
 // Reference reachable_offset (src/lib.rs:409-422).
-int reachable_offset(const t4a_cuda_layout* l, bool maximum, long long* out) {
-  long long total = l->offset;
-  for (int k = 0; k < l->rank; ++k) {
+int reachable_offset(const View& l, bool maximum, long long* out) {
+  long long total = l.offset;
+  for (int k = 0; k < l.rank; ++k) {
     long long step;
-    if (!checked_mul(l->extents[k] - 1, l->strides[k], &step)) return T4A_ERR_OVERFLOW;
+    if (!checked_mul(l.extents[k] - 1, l.strides[k], &step)) return T4A_ERR_OVERFLOW;
     step = maximum ? (step > 0 ? step : 0) : (step < 0 ? step : 0);
     if (!checked_add(total, step, &total)) return T4A_ERR_OVERFLOW;
   }
@@ -74,7 +103,7 @@ int reachable_offset(const t4a_cuda_layout* l, bool maximum, long long* out) {
 }
 
 // Reference LayoutRef::check_span (src/lib.rs:1011-1027).
-int check_span(const t4a_cuda_layout* l, long long len, int esize) {
+int check_span(const View& l, long long len, int esize) {
   if (len < 0) return T4A_ERR_NEGATIVE_COUNT;
   long long count;
   if (int s = element_count(l, &count)) return s;
@@ -88,22 +117,11 @@ int check_span(const t4a_cuda_layout* l, long long len, int esize) {
 }
 
 // Reference require_destination / rejects_broadcast_axis (src/lib.rs:4057-4065, 444-449).
-int require_destination(const t4a_cuda_layout* l) {
-  for (int k = 0; k < l->rank; ++k) {
-    if (l->extents[k] > 1 && l->strides[k] == 0) return T4A_ERR_BROADCAST_DESTINATION;
+int require_destination(const View& l) {
+  for (int k = 0; k < l.rank; ++k) {
+    if (l.extents[k] > 1 && l.strides[k] == 0) return T4A_ERR_BROADCAST_DESTINATION;
   }
   return ok();
-}
-
-// Reference is_compact (src/lib.rs:425-441).
-bool is_compact(const t4a_cuda_layout* l) {
-  if (l->offset != 0) return false;
-  long long stride = 1;
-  for (int k = 0; k < l->rank; ++k) {
-    if (l->strides[k] != stride) return false;
-    if (!checked_mul(stride, l->extents[k], &stride)) return false;
-  }
-  return true;
 }
 
 bool dtype_known(int dtype) { return t4a::dtype_size(dtype) != 0; }
@@ -176,18 +194,18 @@ bool plane_width_ok(unsigned w) { return w == 8 || w == 16 || w == 32; }
 bool combine_width_ok(unsigned w) { return w == 64 || w == 128 || w == 256 || w == 512; }
 
 // Reference reduce_problem (src/lib.rs:3193-3233).
-int reduce_problem(int dtype, int op, const t4a_cuda_layout* out, long long out_len,
-                   const t4a_cuda_layout* in, long long in_len, unsigned axis,
-                   long long* reduce_len, long long* output_len) {
+int reduce_problem(int dtype, int op, const View& out, long long out_len, const View& in,
+                   long long in_len, unsigned axis, long long* reduce_len,
+                   long long* output_len) {
   if (!op_supports(op, dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
-  if (axis >= static_cast<unsigned>(in->rank)) return T4A_ERR_INVALID_AXIS;
-  if (out->rank != in->rank) return T4A_ERR_RANK_LENGTH;
-  for (int k = 0; k < in->rank; ++k) {
+  if (axis >= static_cast<unsigned>(in.rank)) return T4A_ERR_INVALID_AXIS;
+  if (out.rank != in.rank) return T4A_ERR_RANK_LENGTH;
+  for (int k = 0; k < in.rank; ++k) {
     if (static_cast<unsigned>(k) == axis) continue;
-    if (out->extents[k] != in->extents[k]) return T4A_ERR_SHAPE_MISMATCH;
+    if (out.extents[k] != in.extents[k]) return T4A_ERR_SHAPE_MISMATCH;
   }
-  if (out->extents[axis] != 1) return T4A_ERR_SHAPE_MISMATCH;
-  *reduce_len = in->extents[axis];
+  if (out.extents[axis] != 1) return T4A_ERR_SHAPE_MISMATCH;
+  *reduce_len = in.extents[axis];
   if (*reduce_len < 1) return T4A_ERR_NEGATIVE_COUNT;
   if (int s = element_count(out, output_len)) return s;
   if (int s = require_destination(out)) return s;
@@ -231,6 +249,260 @@ int combine_block_width(long long splits) {
   unsigned width = static_cast<unsigned>(kWideCombineMinSplits);
   while (static_cast<long long>(width) < target && width < kMaxBlockWidth) width *= 2;
   return width < kMaxBlockWidth ? width : kMaxBlockWidth;
+}
+
+// Reference RankVariant::select (src/lib.rs:817-838): the general symbol when
+// any participating rank exceeds T4A_CUDA_MAX_RANK.
+void set_variant(t4a_launch* launch, int rank) {
+  launch->variant = rank > T4A_CUDA_MAX_RANK ? T4A_VARIANT_GENERAL : T4A_VARIANT_FAST;
+}
+
+// Movement geometry of any rank: fused first (fuse_move, the fusion move_plan
+// itself applies), then move_plan on the fused axes when at most eight remain;
+// wider geometries are decoded per element by the general twins.
+void movement_geometry(const View& src, const long long* dst_strides, long long dst_offset,
+                       long long len, int es, t4a_launch* launch) {
+  long long fe[t4a::kMaxFusedDims], fs[t4a::kMaxFusedDims], fd[t4a::kMaxFusedDims];
+  const int n = len > 0 ? t4a::fuse_move(src.rank, src.extents, src.strides, dst_strides, fe,
+                                         fs, fd, t4a::kMaxFusedDims)
+                        : 0;
+  if (n >= 0 && n <= t4a::kMaxDims) {
+    t4a::MovePlan plan;
+    t4a::move_plan_view(&plan, n, src.offset, fe, fs, fd, dst_offset, len, es);
+    movement_launch(plan, es, launch);
+  } else {
+    set_launch(launch, blocks_for(len, kBlock * 4), kBlock, 0);
+  }
+  set_variant(launch, src.rank);
+}
+
+// Reference plan_materialize_strided (src/lib.rs:1628-1641) after the layout
+// checks.
+int plan_materialize(int dtype, const View& src, long long src_len, t4a_launch* launch) {
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  long long len;
+  if (int s = element_count(src, &len)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(src, src_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  movement_geometry(src, nullptr, 0, len, es, launch);
+  return ok();
+}
+
+// Reference plan_strided_to_strided (src/lib.rs:1660-1679) after the layout
+// checks.
+int plan_strided(int dtype, const View& src, long long src_len, const View& dst,
+                 long long dst_len, t4a_launch* launch) {
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  bool same = src.rank == dst.rank;
+  for (int k = 0; same && k < src.rank; ++k) same = src.extents[k] == dst.extents[k];
+  if (!same) return T4A_ERR_COUNT_MISMATCH;
+  long long len;
+  if (int s = element_count(src, &len)) return s;
+  if (int s = require_destination(dst)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(src, src_len, es)) return s;
+  if (int s = check_span(dst, dst_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  movement_geometry(src, dst.strides, dst.offset, len, es, launch);
+  return ok();
+}
+
+// A reduction's layouts as a rank <= 8 pair with the same fused dims: the
+// by-value layouts themselves, or for a wider rank the non-axis dims fused
+// (reduce_dims_view) with the axis appended last -- reduce_dims of the pair
+// reproduces those dims. False when more than 7 non-axis dims remain.
+bool reduction_pair(const View& out, const View& in, unsigned axis, t4a_cuda_layout* o8,
+                    t4a_cuda_layout* i8, int* axis8) {
+  std::memset(o8, 0, sizeof(*o8));
+  std::memset(i8, 0, sizeof(*i8));
+  if (in.rank <= T4A_CUDA_MAX_RANK) {
+    o8->rank = out.rank;
+    i8->rank = in.rank;
+    o8->offset = out.offset;
+    i8->offset = in.offset;
+    for (int k = 0; k < in.rank; ++k) {
+      o8->extents[k] = out.extents[k];
+      o8->strides[k] = out.strides[k];
+      i8->extents[k] = in.extents[k];
+      i8->strides[k] = in.strides[k];
+    }
+    *axis8 = static_cast<int>(axis);
+    return true;
+  }
+  t4a::ReduceDimsN<T4A_CUDA_MAX_RANK - 1> rd;
+  if (!t4a::reduce_dims_view(&rd, in.rank, static_cast<int>(axis), out.offset, out.extents,
+                             out.strides, in.offset, in.extents, in.strides))
+    return false;
+  o8->rank = i8->rank = rd.n + 1;
+  o8->offset = out.offset;
+  i8->offset = in.offset;
+  for (int k = 0; k < rd.n; ++k) {
+    o8->extents[k] = i8->extents[k] = rd.ext[k];
+    o8->strides[k] = rd.os[k];
+    i8->strides[k] = rd.is[k];
+  }
+  o8->extents[rd.n] = out.extents[axis];
+  o8->strides[rd.n] = out.strides[axis];
+  i8->extents[rd.n] = in.extents[axis];
+  i8->strides[rd.n] = in.strides[axis];
+  *axis8 = rd.n;
+  return true;
+}
+
+// Reference plan_reduce (src/lib.rs:3318-3338) with check_reduce_width and
+// check_strategy (3288-3316), after the layout checks.
+int plan_reduce(int dtype, int op, int strategy, const View& out, long long out_len,
+                const View& in, long long in_len, unsigned axis, unsigned plane_width,
+                t4a_launch* launch) {
+  if (strategy != T4A_CUDA_REDUCE_UNIT && strategy != T4A_CUDA_REDUCE_PLANE)
+    return T4A_ERR_UNSUPPORTED_OP;
+  if (strategy == T4A_CUDA_REDUCE_UNIT) {
+    if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  } else if (!combine_width_ok(plane_width) && !plane_width_ok(plane_width)) {
+    return T4A_ERR_INVALID_PLANE_WIDTH;
+  }
+  long long reduce_len, output_len;
+  if (int s = reduce_problem(dtype, op, out, out_len, in, in_len, axis, &reduce_len,
+                             &output_len))
+    return s;
+  if (strategy == T4A_CUDA_REDUCE_UNIT && reduce_len > static_cast<long long>(plane_width))
+    return T4A_ERR_STRATEGY_MISMATCH;
+  if (strategy == T4A_CUDA_REDUCE_PLANE && reduce_len < static_cast<long long>(plane_width))
+    return T4A_ERR_STRATEGY_MISMATCH;
+  if (int s = launch_for(strategy, output_len, plane_width, launch)) return s;
+  // A one-group axis in kBlock-thread blocks: threads take several outputs.
+  t4a_cuda_layout o8, i8;
+  int axis8;
+  if (strategy == T4A_CUDA_REDUCE_UNIT && output_len > 0 &&
+      launch->block[0] == static_cast<unsigned>(kBlock) &&
+      reduction_pair(out, in, axis, &o8, &i8, &axis8)) {
+    t4a::ReduceDims rd;
+    t4a::reduce_dims(&rd, o8, i8, axis8);
+    if (t4a::unit_one_group(rd, dtype))
+      set_launch(launch, blocks_for(output_len, kBlock * t4a::kUnitOutputsPerThread), kBlock,
+                 0);
+  }
+  set_variant(launch, in.rank);
+  return ok();
+}
+
+// Reference plan_reduce_partials (src/lib.rs:3340-3431) after the layout checks.
+int plan_reduce_partials(int dtype, int op, const View& partials, long long partials_len,
+                         const View& in, long long in_len, unsigned axis, t4a_split split,
+                         unsigned plane_width, t4a_launch* launch) {
+  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  if (!op_supports(op, dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (axis >= static_cast<unsigned>(in.rank)) return T4A_ERR_INVALID_AXIS;
+  if (partials.rank != in.rank) return T4A_ERR_RANK_LENGTH;
+  for (int k = 0; k < in.rank; ++k) {
+    if (static_cast<unsigned>(k) == axis) continue;
+    if (partials.extents[k] != in.extents[k]) return T4A_ERR_SHAPE_MISMATCH;
+  }
+  const long long reduce_len = in.extents[axis];
+  if (reduce_len < 1) return T4A_ERR_NEGATIVE_COUNT;
+  if (split.splits < 2 || split.chunk_len < static_cast<long long>(plane_width) ||
+      split.chunk_len != reduce_len / split.splits || split.splits > kMaxSplits)
+    return T4A_ERR_INVALID_SPLIT;
+  if (partials.extents[axis] != split.splits) return T4A_ERR_SHAPE_MISMATCH;
+  if (int s = require_destination(partials)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(in, in_len, es)) return s;
+  if (int s = check_span(partials, partials_len, es)) return s;
+  long long output_len = 1;
+  for (int k = 0; k < partials.rank; ++k) {
+    if (static_cast<unsigned>(k) == axis) continue;
+    if (!checked_mul(output_len, partials.extents[k], &output_len)) return T4A_ERR_OVERFLOW;
+  }
+  if (output_len < 0) return T4A_ERR_NEGATIVE_COUNT;
+  long long cubes;
+  if (!checked_mul(output_len, split.splits, &cubes)) return T4A_ERR_OVERFLOW;
+  if (cubes > static_cast<long long>(UINT32_MAX)) return T4A_ERR_LAUNCH_LIMIT;
+  if (cubes > static_cast<long long>(kMaxGridX)) return T4A_ERR_LAUNCH_LIMIT;
+  if (plane_width != static_cast<unsigned>(t4a::kWarp)) {
+    set_launch(launch, cubes, plane_width, 0);
+    if (cubes == 0) launch->grid[1] = launch->grid[2] = 1;
+    set_variant(launch, in.rank);
+    return ok();
+  }
+  t4a_cuda_layout p8, i8;
+  int axis8;
+  if (!reduction_pair(partials, in, axis, &p8, &i8, &axis8)) {
+    // Too many dims for a mapping: the general twin's plane walk, eight
+    // planes per block.
+    set_launch(launch, cubes == 0 ? 0 : blocks_for(cubes, kBlock / t4a::kWarp), kBlock, 0);
+    set_variant(launch, in.rank);
+    return ok();
+  }
+  t4a::PartialsPlan plan;
+  t4a::partials_plan(&plan, p8, i8, axis8, output_len, split.splits, t4a::kWarp,
+                     t4a::sideways_dtype(dtype), es, 16);
+  // Units per block: one (TILES), a plane per 32 lanes (PLANE, VECROWS), a
+  // wavefront per 64 (ROWS).
+  long long per_block = kBlock / t4a::kWave;
+  if (plan.mode == t4a::kPartialsTiles) per_block = 1;
+  if (plan.mode == t4a::kPartialsPlane || plan.mode == t4a::kPartialsVecRows)
+    per_block = kBlock / t4a::kWarp;
+  // Lean planes take one cube each; streaming planes take runs of cubes.
+  if (!t4a::lean_slots(plan, dtype, op, split.splits, split.chunk_len, t4a::kWarp) &&
+      t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))
+    per_block *= t4a::stream_cubes_per_plane(cubes);
+  set_launch(launch, plan.units == 0 ? 0 : blocks_for(plan.units, per_block), kBlock, 0);
+  set_variant(launch, in.rank);
+  return ok();
+}
+
+// Reference plan_reduction (src/lib.rs:3457-3528) with combine_geometry and
+// combine_block_width (3433-3452), after the layout checks. The partials
+// layout is the compact one over the input's extents with the axis replaced by
+// the split count (reference partials_layout_for, src/lib.rs:3530-3557).
+int plan_reduction(int dtype, int op, const View& out, long long out_len, const View& in,
+                   long long in_len, unsigned axis, unsigned plane_width,
+                   t4a_reduction_plan* plan) {
+  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
+  long long reduce_len, output_len;
+  if (int s = reduce_problem(dtype, op, out, out_len, in, in_len, axis, &reduce_len,
+                             &output_len))
+    return s;
+  const int strategy = strategy_for(reduce_len, plane_width);
+  int has_split;
+  t4a_split split;
+  if (int s = t4a_split_policy(reduce_len, plane_width, &has_split, &split)) return s;
+  if (!has_split) {
+    plan->kind = T4A_PLAN_DIRECT;
+    plan->strategy = strategy;
+    return plan_reduce(dtype, op, strategy, out, out_len, in, in_len, axis, plane_width,
+                       &plan->launch);
+  }
+  std::vector<long long> pe(static_cast<size_t>(in.rank)), ps(static_cast<size_t>(in.rank));
+  long long stride = 1;
+  for (int k = 0; k < in.rank; ++k) {
+    pe[k] = static_cast<unsigned>(k) == axis ? split.splits : in.extents[k];
+    ps[k] = stride;
+    if (!checked_mul(stride, pe[k], &stride)) return T4A_ERR_OVERFLOW;
+  }
+  const View partials{in.rank, 0, pe.data(), ps.data()};
+  long long partials_len;
+  if (int s = element_count(partials, &partials_len)) return s;
+  plan->kind = T4A_PLAN_SPLIT;
+  plan->split = split;
+  if (int s = plan_reduce_partials(dtype, op, partials, partials_len, in, in_len, axis, split,
+                                   plane_width, &plan->pass1))
+    return s;
+  const int combine_op = op == T4A_CUDA_REDUCE_SUM_SQUARES ? T4A_CUDA_REDUCE_SUM : op;
+  int combine_strategy;
+  unsigned combine_width;
+  if (combine_op == T4A_CUDA_REDUCE_PROD || split.splits < kWideCombineMinSplits) {
+    combine_strategy = strategy_for(split.splits, plane_width);
+    combine_width = plane_width;
+  } else {
+    combine_strategy = T4A_CUDA_REDUCE_PLANE;
+    combine_width = static_cast<unsigned>(combine_block_width(split.splits));
+  }
+  plan->combine_strategy = combine_strategy;
+  plan->combine_op = combine_op;
+  return plan_reduce(dtype, combine_op, combine_strategy, out, out_len, partials, partials_len,
+                     axis, combine_width, &plan->pass2);
 }
 
 }  // namespace
@@ -293,7 +565,7 @@ int t4a_layout_compact(t4a_cuda_layout* out, int rank, const long long* extents)
 int t4a_layout_element_count(const t4a_cuda_layout* layout, long long* count) {
   if (count == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_layout(layout)) return s;
-  return element_count(layout, count);
+  return element_count(V(layout), count);
 }
 
 // Reference plan_copy_exact -> plan_elementwise (src/lib.rs:1592-1599, 1624-1626): every
@@ -313,16 +585,14 @@ int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long lon
                                  t4a_launch* launch) {
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_layout(src)) return s;
-  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
-  long long len;
-  if (int s = element_count(src, &len)) return s;
-  const int es = t4a::dtype_size(dtype);
-  if (int s = check_span(src, src_len, es)) return s;
-  if (int s = flat_launch_check(len)) return s;
-  t4a::MovePlan plan;
-  t4a::move_plan(&plan, *src, nullptr, 0, len, es);
-  movement_launch(plan, es, launch);
-  return ok();
+  return plan_materialize(dtype, V(src), src_len, launch);
+}
+
+int t4a_plan_materialize_strided_any(int dtype, const t4a_cuda_layout_any* src,
+                                     long long src_len, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(src)) return s;
+  return plan_materialize(dtype, V(src), src_len, launch);
 }
 
 // Reference plan_strided_to_strided (src/lib.rs:1660-1679).
@@ -332,21 +602,16 @@ int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_layout(src)) return s;
   if (int s = check_layout(dst)) return s;
-  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
-  bool same = src->rank == dst->rank;
-  for (int k = 0; same && k < src->rank; ++k) same = src->extents[k] == dst->extents[k];
-  if (!same) return T4A_ERR_COUNT_MISMATCH;
-  long long len;
-  if (int s = element_count(src, &len)) return s;
-  if (int s = require_destination(dst)) return s;
-  const int es = t4a::dtype_size(dtype);
-  if (int s = check_span(src, src_len, es)) return s;
-  if (int s = check_span(dst, dst_len, es)) return s;
-  if (int s = flat_launch_check(len)) return s;
-  t4a::MovePlan plan;
-  t4a::move_plan(&plan, *src, dst->strides, dst->offset, len, es);
-  movement_launch(plan, es, launch);
-  return ok();
+  return plan_strided(dtype, V(src), src_len, V(dst), dst_len, launch);
+}
+
+int t4a_plan_strided_to_strided_any(int dtype, const t4a_cuda_layout_any* src,
+                                    long long src_len, const t4a_cuda_layout_any* dst,
+                                    long long dst_len, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(src)) return s;
+  if (int s = check_any(dst)) return s;
+  return plan_strided(dtype, V(src), src_len, V(dst), dst_len, launch);
 }
 
 // Reference TransposeConfig::new (src/lib.rs:471-491).
@@ -446,32 +711,19 @@ int t4a_plan_reduce(int dtype, int op, int strategy, const t4a_cuda_layout* out_
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_layout(out_layout)) return s;
   if (int s = check_layout(in_layout)) return s;
-  if (strategy != T4A_CUDA_REDUCE_UNIT && strategy != T4A_CUDA_REDUCE_PLANE)
-    return T4A_ERR_UNSUPPORTED_OP;
-  if (strategy == T4A_CUDA_REDUCE_UNIT) {
-    if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
-  } else if (!combine_width_ok(plane_width) && !plane_width_ok(plane_width)) {
-    return T4A_ERR_INVALID_PLANE_WIDTH;
-  }
-  long long reduce_len, output_len;
-  if (int s = reduce_problem(dtype, op, out_layout, out_len, in_layout, in_len, axis,
-                             &reduce_len, &output_len))
-    return s;
-  if (strategy == T4A_CUDA_REDUCE_UNIT && reduce_len > static_cast<long long>(plane_width))
-    return T4A_ERR_STRATEGY_MISMATCH;
-  if (strategy == T4A_CUDA_REDUCE_PLANE && reduce_len < static_cast<long long>(plane_width))
-    return T4A_ERR_STRATEGY_MISMATCH;
-  if (int s = launch_for(strategy, output_len, plane_width, launch)) return s;
-  // A one-group axis in kBlock-thread blocks: threads take several outputs.
-  if (strategy == T4A_CUDA_REDUCE_UNIT && output_len > 0 &&
-      launch->block[0] == static_cast<unsigned>(kBlock)) {
-    t4a::ReduceDims rd;
-    t4a::reduce_dims(&rd, *out_layout, *in_layout, static_cast<int>(axis));
-    if (t4a::unit_one_group(rd, dtype))
-      set_launch(launch, blocks_for(output_len, kBlock * t4a::kUnitOutputsPerThread), kBlock,
-                 0);
-  }
-  return ok();
+  return plan_reduce(dtype, op, strategy, V(out_layout), out_len, V(in_layout), in_len, axis,
+                     plane_width, launch);
+}
+
+int t4a_plan_reduce_any(int dtype, int op, int strategy, const t4a_cuda_layout_any* out_layout,
+                        long long out_len, const t4a_cuda_layout_any* in_layout,
+                        long long in_len, unsigned int axis, unsigned int plane_width,
+                        t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(out_layout)) return s;
+  if (int s = check_any(in_layout)) return s;
+  return plan_reduce(dtype, op, strategy, V(out_layout), out_len, V(in_layout), in_len, axis,
+                     plane_width, launch);
 }
 
 // Reference plan_reduce_partials (src/lib.rs:3340-3431). A 32-lane plan runs
@@ -484,55 +736,19 @@ int t4a_plan_reduce_partials(int dtype, int op, const t4a_cuda_layout* partials_
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_layout(partials_layout)) return s;
   if (int s = check_layout(in_layout)) return s;
-  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
-  if (!op_supports(op, dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
-  if (axis >= static_cast<unsigned>(in_layout->rank)) return T4A_ERR_INVALID_AXIS;
-  if (partials_layout->rank != in_layout->rank) return T4A_ERR_RANK_LENGTH;
-  for (int k = 0; k < in_layout->rank; ++k) {
-    if (static_cast<unsigned>(k) == axis) continue;
-    if (partials_layout->extents[k] != in_layout->extents[k]) return T4A_ERR_SHAPE_MISMATCH;
-  }
-  const long long reduce_len = in_layout->extents[axis];
-  if (reduce_len < 1) return T4A_ERR_NEGATIVE_COUNT;
-  if (split.splits < 2 || split.chunk_len < static_cast<long long>(plane_width) ||
-      split.chunk_len != reduce_len / split.splits || split.splits > kMaxSplits)
-    return T4A_ERR_INVALID_SPLIT;
-  if (partials_layout->extents[axis] != split.splits) return T4A_ERR_SHAPE_MISMATCH;
-  if (int s = require_destination(partials_layout)) return s;
-  const int es = t4a::dtype_size(dtype);
-  if (int s = check_span(in_layout, in_len, es)) return s;
-  if (int s = check_span(partials_layout, partials_len, es)) return s;
-  long long output_len = 1;
-  for (int k = 0; k < partials_layout->rank; ++k) {
-    if (static_cast<unsigned>(k) == axis) continue;
-    if (!checked_mul(output_len, partials_layout->extents[k], &output_len))
-      return T4A_ERR_OVERFLOW;
-  }
-  if (output_len < 0) return T4A_ERR_NEGATIVE_COUNT;
-  long long cubes;
-  if (!checked_mul(output_len, split.splits, &cubes)) return T4A_ERR_OVERFLOW;
-  if (cubes > static_cast<long long>(UINT32_MAX)) return T4A_ERR_LAUNCH_LIMIT;
-  if (cubes > static_cast<long long>(kMaxGridX)) return T4A_ERR_LAUNCH_LIMIT;
-  if (plane_width != static_cast<unsigned>(t4a::kWarp)) {
-    set_launch(launch, cubes, plane_width, 0);
-    if (cubes == 0) launch->grid[1] = launch->grid[2] = 1;
-    return ok();
-  }
-  t4a::PartialsPlan plan;
-  t4a::partials_plan(&plan, *partials_layout, *in_layout, static_cast<int>(axis), output_len,
-                     split.splits, t4a::kWarp, t4a::sideways_dtype(dtype), es, 16);
-  // Units per block: one (TILES), a plane per 32 lanes (PLANE, VECROWS), a
-  // wavefront per 64 (ROWS).
-  long long per_block = kBlock / t4a::kWave;
-  if (plan.mode == t4a::kPartialsTiles) per_block = 1;
-  if (plan.mode == t4a::kPartialsPlane || plan.mode == t4a::kPartialsVecRows)
-    per_block = kBlock / t4a::kWarp;
-  // Lean planes take one cube each; streaming planes take runs of cubes.
-  if (!t4a::lean_slots(plan, dtype, op, split.splits, split.chunk_len, t4a::kWarp) &&
-      t4a::stream_applies(plan, dtype, op, split.chunk_len, t4a::kWarp))
-    per_block *= t4a::stream_cubes_per_plane(cubes);
-  set_launch(launch, plan.units == 0 ? 0 : blocks_for(plan.units, per_block), kBlock, 0);
-  return ok();
+  return plan_reduce_partials(dtype, op, V(partials_layout), partials_len, V(in_layout), in_len,
+                              axis, split, plane_width, launch);
+}
+
+int t4a_plan_reduce_partials_any(int dtype, int op, const t4a_cuda_layout_any* partials_layout,
+                                 long long partials_len, const t4a_cuda_layout_any* in_layout,
+                                 long long in_len, unsigned int axis, t4a_split split,
+                                 unsigned int plane_width, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(partials_layout)) return s;
+  if (int s = check_any(in_layout)) return s;
+  return plan_reduce_partials(dtype, op, V(partials_layout), partials_len, V(in_layout), in_len,
+                              axis, split, plane_width, launch);
 }
 
 // Reference plan_reduction (src/lib.rs:3457-3528) with combine_geometry and
@@ -544,44 +760,20 @@ int t4a_plan_reduction(int dtype, int op, const t4a_cuda_layout* out_layout, lon
   std::memset(plan, 0, sizeof(*plan));
   if (int s = check_layout(out_layout)) return s;
   if (int s = check_layout(in_layout)) return s;
-  if (!plane_width_ok(plane_width)) return T4A_ERR_INVALID_PLANE_WIDTH;
-  long long reduce_len, output_len;
-  if (int s = reduce_problem(dtype, op, out_layout, out_len, in_layout, in_len, axis,
-                             &reduce_len, &output_len))
-    return s;
-  const int strategy = strategy_for(reduce_len, plane_width);
-  int has_split;
-  t4a_split split;
-  if (int s = t4a_split_policy(reduce_len, plane_width, &has_split, &split)) return s;
-  if (!has_split) {
-    plan->kind = T4A_PLAN_DIRECT;
-    plan->strategy = strategy;
-    return t4a_plan_reduce(dtype, op, strategy, out_layout, out_len, in_layout, in_len, axis,
-                           plane_width, &plan->launch);
-  }
-  t4a_cuda_layout partials;
-  if (int s = t4a_reduction_partials_layout(in_layout, axis, split.splits, &partials)) return s;
-  long long partials_len;
-  if (int s = element_count(&partials, &partials_len)) return s;
-  plan->kind = T4A_PLAN_SPLIT;
-  plan->split = split;
-  if (int s = t4a_plan_reduce_partials(dtype, op, &partials, partials_len, in_layout, in_len,
-                                       axis, split, plane_width, &plan->pass1))
-    return s;
-  const int combine_op = op == T4A_CUDA_REDUCE_SUM_SQUARES ? T4A_CUDA_REDUCE_SUM : op;
-  int combine_strategy;
-  unsigned combine_width;
-  if (combine_op == T4A_CUDA_REDUCE_PROD || split.splits < kWideCombineMinSplits) {
-    combine_strategy = strategy_for(split.splits, plane_width);
-    combine_width = plane_width;
-  } else {
-    combine_strategy = T4A_CUDA_REDUCE_PLANE;
-    combine_width = static_cast<unsigned>(combine_block_width(split.splits));
-  }
-  plan->combine_strategy = combine_strategy;
-  plan->combine_op = combine_op;
-  return t4a_plan_reduce(dtype, combine_op, combine_strategy, out_layout, out_len, &partials,
-                         partials_len, axis, combine_width, &plan->pass2);
+  return plan_reduction(dtype, op, V(out_layout), out_len, V(in_layout), in_len, axis,
+                        plane_width, plan);
+}
+
+int t4a_plan_reduction_any(int dtype, int op, const t4a_cuda_layout_any* out_layout,
+                           long long out_len, const t4a_cuda_layout_any* in_layout,
+                           long long in_len, unsigned int axis, unsigned int plane_width,
+                           t4a_reduction_plan* plan) {
+  if (plan == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  std::memset(plan, 0, sizeof(*plan));
+  if (int s = check_any(out_layout)) return s;
+  if (int s = check_any(in_layout)) return s;
+  return plan_reduction(dtype, op, V(out_layout), out_len, V(in_layout), in_len, axis,
+                        plane_width, plan);
 }
 
 // Reference reduction_partials_layout / partials_layout_for (src/lib.rs:3530-3557).
@@ -594,6 +786,28 @@ int t4a_reduction_partials_layout(const t4a_cuda_layout* in_layout, unsigned int
   for (int k = 0; k < in_layout->rank; ++k) extents[k] = in_layout->extents[k];
   extents[axis] = splits;
   return t4a_layout_compact(partials_layout, in_layout->rank, extents);
+}
+
+// The same for any rank: the compact partials layout's `rank` extents and
+// strides into the caller's arrays (its offset is 0).
+int t4a_reduction_partials_layout_any(const t4a_cuda_layout_any* in_layout, unsigned int axis,
+                                      long long splits, long long* extents,
+                                      long long* strides) {
+  if (int s = check_any(in_layout)) return s;
+  if (axis >= static_cast<unsigned>(in_layout->rank)) return T4A_ERR_INVALID_AXIS;
+  if (extents == nullptr || strides == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  // As t4a_layout_compact: the strides (overflow) first, then the extents.
+  long long stride = 1;
+  for (int k = 0; k < in_layout->rank; ++k) {
+    const long long e = static_cast<unsigned>(k) == axis ? splits : in_layout->extents[k];
+    extents[k] = e;
+    strides[k] = stride;
+    if (!checked_mul(stride, e, &stride)) return T4A_ERR_OVERFLOW;
+  }
+  for (int k = 0; k < in_layout->rank; ++k) {
+    if (extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
+  }
+  return ok();
 }
 
 }  // extern "C"

@@ -64,8 +64,9 @@ struct alignas(16) Group {
 // The loop runs over the fixed maximum rank so every field index is a
 // compile-time constant: a runtime subscript would copy the by-value plan into
 // per-lane scratch memory.
-__device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
-                                              long long* in_base, long long* out_off) {
+template <typename RD>
+__device__ __forceinline__ void decode_output(const RD& rd, long long o, long long* in_base,
+                                              long long* out_off) {
   long long ib = rd.in_offset;
   long long ob = rd.out_offset;
   // Quotients in 32 bits when every output index fits (rd.narrow: the extent
@@ -73,9 +74,7 @@ __device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
   // costs several times a 32-bit one.
   const bool narrow = rd.narrow;
   unsigned int o32 = static_cast<unsigned int>(o);
-#pragma unroll
-  for (int k = 0; k < kMaxDims; ++k) {
-    if (k >= rd.n) break;
+  auto digit = [&](int k) {
     long long c;
     if (k + 1 == rd.n) {
       c = narrow ? static_cast<long long>(o32) : o;
@@ -90,6 +89,16 @@ __device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
     }
     ib += c * rd.is[k];
     ob += c * rd.os[k];
+  };
+  if constexpr (RD::kDims <= kMaxDims) {
+#pragma unroll
+    for (int k = 0; k < RD::kDims; ++k) {
+      if (k >= rd.n) break;
+      digit(k);
+    }
+  } else {
+    // The general-rank dims live in LDS: a runtime subscript is an LDS read.
+    for (int k = 0; k < rd.n; ++k) digit(k);
   }
   *in_base = ib;
   *out_off = ob;
@@ -99,9 +108,9 @@ __device__ __forceinline__ void decode_output(const ReduceDims& rd, long long o,
 // One thread per output, serial fold from element 0 (reference reduce.cu:196-224).
 // On a contiguous axis whose every output starts 16-byte aligned, the elements
 // arrive as 16-byte groups; the fold order is unchanged.
-template <typename Fold, typename T, bool Vector, int BS>
+template <typename Fold, typename T, bool Vector, int BS, typename RD>
 __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __restrict__ in,
-                                             const ReduceDims& rd, long long output_len,
+                                             const RD& rd, long long output_len,
                                              Fold f) {
   const long long len = rd.axis_len;
   const long long stride = rd.axis_stride;
@@ -179,10 +188,10 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
 // UNIT over a one-group axis (unit_one_group) in kBlock blocks: each thread
 // takes outputs o, o + G, o + 2G, o + 3G (G the grid's thread count), issues
 // their 16-byte loads together, then folds each output serially from element 0.
-template <typename Fold, typename T>
+template <typename Fold, typename T, typename RD>
 __device__ __forceinline__ void unit_outputs_grouped(T* __restrict__ out,
                                                      const T* __restrict__ in,
-                                                     const ReduceDims& rd, long long output_len,
+                                                     const RD& rd, long long output_len,
                                                      Fold f) {
   constexpr int V = VecLanes<T>::value;
   constexpr int U = kUnitOutputsPerThread;
@@ -215,8 +224,8 @@ __device__ __forceinline__ void unit_outputs_grouped(T* __restrict__ out,
   }
 }
 
-template <typename Fold, typename T, int BS>
-__device__ __forceinline__ void unit_body(void* out, const void* in, const ReduceDims& rd,
+template <typename Fold, typename T, int BS, typename RD>
+__device__ __forceinline__ void unit_body(void* out, const void* in, const RD& rd,
                                           long long output_len, Fold f) {
   T* o = static_cast<T*>(out);
   const T* x = static_cast<const T*>(in);
@@ -224,8 +233,7 @@ __device__ __forceinline__ void unit_body(void* out, const void* in, const Reduc
     constexpr int V = VecLanes<T>::value;
     bool vector = rd.axis_stride == 1 && rd.axis_len >= V && rd.in_offset % V == 0 &&
                   (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-#pragma unroll
-    for (int k = 0; k < kMaxDims; ++k) vector = vector && (k >= rd.n || rd.is[k] % V == 0);
+    for (int k = 0; k < rd.n; ++k) vector = vector && rd.is[k] % V == 0;
     if (vector) {
       if constexpr (BS == kBlock) {
         if (rd.axis_len < 2 * V) {
@@ -380,10 +388,9 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
 // W <= 32: the xor tree. W = 64..512: the xor tree inside each 32-lane warp,
 // warp results through LDS, then warp 0 folds them with the xor tree over the
 // first W / 32 lanes (reference reduce.cu:170-194).
-template <typename Fold, typename T>
-__device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr,
-                                           const ReduceDims& rd, long long output_len, Fold f,
-                                           unsigned char* lds) {
+template <typename Fold, typename T, typename RD>
+__device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, const RD& rd,
+                                           long long output_len, Fold f, unsigned char* lds) {
   T* out = static_cast<T*>(out_ptr);
   const T* in = static_cast<const T*>(in_ptr);
   T* warp_results = reinterpret_cast<T*>(lds);
@@ -840,17 +847,17 @@ __device__ __forceinline__ void reduction_joined(void* partials_ptr, const void*
 // PLANE mapping: plane = W lanes (W = blockDim.x when blockDim.x <= 32, else 32
 // with blockDim.x / 32 planes per block, reference reduce.cu:557-581); planes
 // stride over the cubes.
-template <typename Fold, typename T>
-__device__ __forceinline__ void partials_planes(void* partials_ptr, const void* in_ptr,
-                                                const PartialsPlan& pp, long long output_len,
-                                                long long splits, long long chunk_len, Fold f) {
+template <typename Fold, typename T, typename RD>
+__device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const void* in_ptr,
+                                                     const RD& rd, long long output_len,
+                                                     long long splits, long long chunk_len,
+                                                     Fold f) {
   T* partials = static_cast<T*>(partials_ptr);
   const T* in = static_cast<const T*>(in_ptr);
   const int w = blockDim.x <= static_cast<unsigned>(kWarp) ? static_cast<int>(blockDim.x) : kWarp;
   const int planes = static_cast<int>(blockDim.x) / w;
   const int lane = static_cast<int>(threadIdx.x) % w;
   const long long cubes = output_len * splits;
-  const ReduceDims& rd = pp.dims;
   for (long long cube = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
        cube < cubes; cube += static_cast<long long>(gridDim.x) * planes) {
     const long long o = cube / splits;
@@ -864,6 +871,14 @@ __device__ __forceinline__ void partials_planes(void* partials_ptr, const void* 
     const T reduced = plane_tree(acc, w, f);
     if (lane == 0) partials[pb] = reduced;
   }
+}
+
+template <typename Fold, typename T>
+__device__ __forceinline__ void partials_planes(void* partials_ptr, const void* in_ptr,
+                                                const PartialsPlan& pp, long long output_len,
+                                                long long splits, long long chunk_len, Fold f) {
+  partials_planes_dims<Fold, T>(partials_ptr, in_ptr, pp.dims, output_len, splits, chunk_len,
+                                f);
 }
 
 // Unit `u` of the COLUMNS/ROWS mappings: column block fastest, then the split,
@@ -1250,9 +1265,9 @@ __device__ __forceinline__ void dispatch_dtype(int dtype, Fn&& fn) {
   }
 }
 
-template <typename T>
+template <typename T, typename RD>
 __device__ __forceinline__ void reduce_run(void* out, const void* in, int op, bool plane,
-                                           const ReduceDims& rd, long long output_len,
+                                           const RD& rd, long long output_len,
                                            unsigned char* warp_lds) {
   dispatch_fold<T>(op, [&](auto fold) {
     if (plane) {
@@ -1399,6 +1414,56 @@ extern "C" __global__ void __launch_bounds__(256)
     t4a::dispatch_fold<T>(op, [&](auto fold) {
       t4a::partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
                                               fold);
+    });
+  });
+}
+
+// General-rank twins (reference reduce.cu:854-940, docs/abi/c-kernel-abi.md
+// "Dynamic rank"): the geometry arrays live in caller-owned device memory.
+// Thread 0 fuses them into LDS dims (at most 62 remain for any layout of fewer
+// than 2^63 elements) and the block runs the by-value entries' bodies on them,
+// so the results are the fast twins' bits. An axis outside the rank, or ranks
+// that differ, do no work.
+__device__ __forceinline__ void any_dims(t4a::ReduceDimsWide* rd, const t4a_cuda_layout_any& out,
+                                         const t4a_cuda_layout_any& in, int axis) {
+  if (axis < 0 || axis >= in.rank || out.rank != in.rank) {
+    rd->n = -1;
+    return;
+  }
+  t4a::reduce_dims_view(rd, in.rank, axis, out.offset, out.extents, out.strides, in.offset,
+                        in.extents, in.strides);
+}
+
+extern "C" __global__ void __launch_bounds__(512)
+    t4a_cuda_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
+                        t4a_cuda_layout_any out_layout, t4a_cuda_layout_any in_layout, int axis,
+                        long long output_len) {
+  __shared__ t4a::ReduceDimsWide rd;
+  __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
+  if (threadIdx.x == 0) any_dims(&rd, out_layout, in_layout, axis);
+  __syncthreads();
+  if (rd.n < 0) return;
+  const bool plane = strategy == T4A_CUDA_REDUCE_PLANE;
+  t4a::dispatch_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds);
+  });
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_reduce_partials_any(void* partials, const void* in, int dtype, int op,
+                                 t4a_cuda_layout_any partials_layout,
+                                 t4a_cuda_layout_any in_layout, int axis, long long output_len,
+                                 long long splits, long long chunk_len) {
+  __shared__ t4a::ReduceDimsWide rd;
+  if (threadIdx.x == 0) any_dims(&rd, partials_layout, in_layout, axis);
+  __syncthreads();
+  if (rd.n < 0) return;
+  t4a::dispatch_dtype(dtype, [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    t4a::dispatch_fold<T>(op, [&](auto fold) {
+      t4a::partials_planes_dims<decltype(fold), T>(partials, in, rd, output_len, splits,
+                                                   chunk_len, fold);
     });
   });
 }
@@ -1831,4 +1896,39 @@ extern "C" int t4a_hip_reduction_joins(const void* in, int dtype, int op,
   return joined_applies(in, dtype, op, *out_layout, *in_layout, pl, axis, output_len, *plan, &j)
              ? 1
              : 0;
+}
+
+// The general-rank twins on the caller's stream with a planned geometry (any
+// t4a_plan_*_any geometry: the twins stride over their work).
+extern "C" int t4a_hip_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
+                                  const t4a_cuda_layout_any* out_layout,
+                                  const t4a_cuda_layout_any* in_layout, int axis,
+                                  long long output_len, const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  hipLaunchKernelGGL(t4a_cuda_reduce_any, grid, block, 0, static_cast<hipStream_t>(stream), out,
+                     in, dtype, op, strategy, *out_layout, *in_layout, axis, output_len);
+  return status_of_last_launch();
+}
+
+extern "C" int t4a_hip_reduce_partials_any(void* partials, const void* in, int dtype, int op,
+                                           const t4a_cuda_layout_any* partials_layout,
+                                           const t4a_cuda_layout_any* in_layout, int axis,
+                                           long long output_len, long long splits,
+                                           long long chunk_len, const t4a_launch* launch,
+                                           void* stream) {
+  if (launch == nullptr || partials_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (partials == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  hipLaunchKernelGGL(t4a_cuda_reduce_partials_any, grid, block, 0,
+                     static_cast<hipStream_t>(stream), partials, in, dtype, op,
+                     *partials_layout, *in_layout, axis, output_len, splits, chunk_len);
+  return status_of_last_launch();
 }

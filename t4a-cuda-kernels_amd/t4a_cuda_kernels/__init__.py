@@ -16,7 +16,7 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import CLaunch, CLayout, CReductionPlan, CSplit, CTransposeConfig
+from ._lib import CLaunch, CLayout, CLayoutAny, CReductionPlan, CSplit, CTransposeConfig
 
 MAX_RANK = 8
 ABI_REVISION = 14
@@ -224,6 +224,104 @@ class Layout:
         return f"Layout(extents={self.extents}, strides={self.strides}, offset={self.offset})"
 
 
+class WideLayout:
+    """Strided layout of any rank, axis 0 fastest (reference WideLayout,
+    src/lib.rs:1066-1110, validated as LayoutRef::new, 908-928): the geometry of
+    the general-rank `_any` twins. The planners read it from host memory
+    (`host_c`); the launchers take a `t4a_cuda_layout_any` whose arrays the
+    caller has copied to the device (`device_c`, `pack`)."""
+
+    __slots__ = ("_ext", "_str", "_offset")
+
+    def __init__(self, extents: Sequence[int], strides: Sequence[int], offset: int = 0):
+        if len(extents) != len(strides):
+            raise T4aError(Error.RankLength + 1)
+        if any(e < 0 for e in extents):
+            raise T4aError(Error.NegativeExtent + 1)
+        self._ext = [int(e) for e in extents]
+        self._str = [int(x) for x in strides]
+        self._offset = int(offset)
+
+    @classmethod
+    def compact(cls, extents: Sequence[int]) -> "WideLayout":
+        strides, stride = [], 1
+        for e in extents:
+            strides.append(stride)
+            stride *= e
+            if stride >= 2**63:
+                raise T4aError(Error.Overflow + 1)
+        return cls(extents, strides, 0)
+
+    @classmethod
+    def of(cls, layout: "Layout") -> "WideLayout":
+        return cls(layout.extents, layout.strides, layout.offset)
+
+    @property
+    def rank(self) -> int:
+        return len(self._ext)
+
+    @property
+    def offset(self) -> int:
+        return self._offset
+
+    @property
+    def extents(self) -> list[int]:
+        return list(self._ext)
+
+    @property
+    def strides(self) -> list[int]:
+        return list(self._str)
+
+    def element_count(self) -> int:
+        n = 1
+        for e in self._ext:
+            n *= e
+            if n >= 2**63:
+                raise T4aError(Error.Overflow + 1)
+        return n
+
+    def max_reachable_offset(self) -> int:
+        return self._offset + sum(max((e - 1) * s, 0) for e, s in zip(self._ext, self._str))
+
+    def min_reachable_offset(self) -> int:
+        return self._offset + sum(min((e - 1) * s, 0) for e, s in zip(self._ext, self._str))
+
+    def pack(self) -> list[int]:
+        """The extents, then the strides (reference LayoutRef::pack, src/lib.rs:1029-1038)."""
+        return self._ext + self._str
+
+    def host_c(self) -> CLayoutAny:
+        """A t4a_cuda_layout_any over host copies of the arrays (kept alive by
+        the returned struct), for the t4a_plan_*_any planners."""
+        n = max(self.rank, 1)
+        ext = (c_longlong * n)(*self._ext)
+        st = (c_longlong * n)(*self._str)
+        c = CLayoutAny()
+        c.rank = self.rank
+        c.offset = self._offset
+        c.extents = ctypes.addressof(ext)
+        c.strides = ctypes.addressof(st)
+        c._keep = (ext, st)  # the arrays live as long as the struct
+        return c
+
+    def device_c(self, extents_ptr: int, strides_ptr: int) -> CLayoutAny:
+        """The launchers' t4a_cuda_layout_any: the arrays at `extents_ptr` and
+        `strides_ptr`, device copies the caller made of `extents` / `strides`."""
+        c = CLayoutAny()
+        c.rank = self.rank
+        c.offset = self._offset
+        c.extents = extents_ptr
+        c.strides = strides_ptr
+        return c
+
+    def __eq__(self, other: object) -> bool:
+        return (isinstance(other, WideLayout) and self._ext == other._ext
+                and self._str == other._str and self._offset == other._offset)
+
+    def __repr__(self) -> str:
+        return f"WideLayout(extents={self._ext}, strides={self._str}, offset={self._offset})"
+
+
 @dataclass(frozen=True)
 class TransposeConfig:
     """Tiled-transpose configuration (reference src/lib.rs:452-517)."""
@@ -327,18 +425,36 @@ def plan_copy_exact(dtype: DType, length: int) -> Launch:
     return Launch.from_c(out)
 
 
-def plan_materialize_strided(dtype: DType, src: Layout, src_len: int) -> Launch:
+def _wide(*layouts) -> bool:
+    """Whether a call takes the general-rank planners: any WideLayout operand."""
+    return any(isinstance(x, WideLayout) for x in layouts)
+
+
+def _any(x) -> CLayoutAny:
+    return (x if isinstance(x, WideLayout) else WideLayout.of(x)).host_c()
+
+
+def plan_materialize_strided(dtype: DType, src, src_len: int) -> Launch:
     out = CLaunch()
-    _check(_lib.load().t4a_plan_materialize_strided(int(dtype), byref(_layout(src)), src_len,
-                                                    byref(out)))
+    if _wide(src):
+        _check(_lib.load().t4a_plan_materialize_strided_any(int(dtype), byref(_any(src)),
+                                                            src_len, byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_materialize_strided(int(dtype), byref(_layout(src)),
+                                                        src_len, byref(out)))
     return Launch.from_c(out)
 
 
-def plan_strided_to_strided(dtype: DType, src: Layout, src_len: int, dst: Layout,
-                            dst_len: int) -> Launch:
+def plan_strided_to_strided(dtype: DType, src, src_len: int, dst, dst_len: int) -> Launch:
     out = CLaunch()
-    _check(_lib.load().t4a_plan_strided_to_strided(int(dtype), byref(_layout(src)), src_len,
-                                                   byref(_layout(dst)), dst_len, byref(out)))
+    if _wide(src, dst):
+        _check(_lib.load().t4a_plan_strided_to_strided_any(int(dtype), byref(_any(src)), src_len,
+                                                           byref(_any(dst)), dst_len,
+                                                           byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_strided_to_strided(int(dtype), byref(_layout(src)), src_len,
+                                                       byref(_layout(dst)), dst_len,
+                                                       byref(out)))
     return Launch.from_c(out)
 
 
@@ -363,10 +479,16 @@ def plan_reduce(dtype: DType, op: ReduceOp, strategy: ReduceStrategy, out_layout
                 out_len: int, in_layout: Layout, in_len: int, axis: int,
                 plane_width: int) -> Launch:
     out = CLaunch()
-    _check(_lib.load().t4a_plan_reduce(int(dtype), int(op), int(strategy),
-                                       byref(_layout(out_layout)), out_len,
-                                       byref(_layout(in_layout)), in_len, axis, plane_width,
-                                       byref(out)))
+    if _wide(out_layout, in_layout):
+        _check(_lib.load().t4a_plan_reduce_any(int(dtype), int(op), int(strategy),
+                                               byref(_any(out_layout)), out_len,
+                                               byref(_any(in_layout)), in_len, axis, plane_width,
+                                               byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_reduce(int(dtype), int(op), int(strategy),
+                                           byref(_layout(out_layout)), out_len,
+                                           byref(_layout(in_layout)), in_len, axis, plane_width,
+                                           byref(out)))
     return Launch.from_c(out)
 
 
@@ -374,10 +496,18 @@ def plan_reduce_partials(dtype: DType, op: ReduceOp, partials_layout: Layout,
                          partials_len: int, in_layout: Layout, in_len: int, axis: int,
                          split: Split, plane_width: int) -> Launch:
     out = CLaunch()
-    _check(_lib.load().t4a_plan_reduce_partials(int(dtype), int(op),
-                                                byref(_layout(partials_layout)), partials_len,
-                                                byref(_layout(in_layout)), in_len, axis,
-                                                split.to_c(), plane_width, byref(out)))
+    if _wide(partials_layout, in_layout):
+        _check(_lib.load().t4a_plan_reduce_partials_any(int(dtype), int(op),
+                                                        byref(_any(partials_layout)),
+                                                        partials_len, byref(_any(in_layout)),
+                                                        in_len, axis, split.to_c(), plane_width,
+                                                        byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_reduce_partials(int(dtype), int(op),
+                                                    byref(_layout(partials_layout)),
+                                                    partials_len, byref(_layout(in_layout)),
+                                                    in_len, axis, split.to_c(), plane_width,
+                                                    byref(out)))
     return Launch.from_c(out)
 
 
@@ -385,9 +515,14 @@ def plan_reduction(dtype: DType, op: ReduceOp, out_layout: Layout, out_len: int,
                    in_layout: Layout, in_len: int, axis: int,
                    plane_width: int) -> ReductionPlan:
     p = CReductionPlan()
-    _check(_lib.load().t4a_plan_reduction(int(dtype), int(op), byref(_layout(out_layout)),
-                                          out_len, byref(_layout(in_layout)), in_len, axis,
-                                          plane_width, byref(p)))
+    if _wide(out_layout, in_layout):
+        _check(_lib.load().t4a_plan_reduction_any(int(dtype), int(op), byref(_any(out_layout)),
+                                                  out_len, byref(_any(in_layout)), in_len, axis,
+                                                  plane_width, byref(p)))
+    else:
+        _check(_lib.load().t4a_plan_reduction(int(dtype), int(op), byref(_layout(out_layout)),
+                                              out_len, byref(_layout(in_layout)), in_len, axis,
+                                              plane_width, byref(p)))
     if p.kind == 0:
         return ReductionPlan("Direct", strategy=ReduceStrategy(p.strategy),
                              launch=Launch.from_c(p.launch))
@@ -397,7 +532,14 @@ def plan_reduction(dtype: DType, op: ReduceOp, out_layout: Layout, out_len: int,
                          combine_op=ReduceOp(p.combine_op), pass2=Launch.from_c(p.pass2))
 
 
-def reduction_partials_layout(in_layout: Layout, axis: int, splits: int) -> Layout:
+def reduction_partials_layout(in_layout, axis: int, splits: int):
+    """The compact partials layout; a WideLayout for a WideLayout input."""
+    if _wide(in_layout):
+        n = max(in_layout.rank, 1)
+        ext, st = (c_longlong * n)(), (c_longlong * n)()
+        _check(_lib.load().t4a_reduction_partials_layout_any(byref(_any(in_layout)), axis, splits,
+                                                             ext, st))
+        return WideLayout(list(ext[: in_layout.rank]), list(st[: in_layout.rank]), 0)
     out = CLayout()
     _check(_lib.load().t4a_reduction_partials_layout(byref(_layout(in_layout)), axis, splits,
                                                      byref(out)))

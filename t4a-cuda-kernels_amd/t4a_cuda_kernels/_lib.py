@@ -25,6 +25,20 @@ class CLayout(ctypes.Structure):
     ]
 
 
+class CLayoutAny(ctypes.Structure):
+    """t4a_cuda_layout_any: 32 bytes, the arrays by pointer (reference
+    cuda/include/t4a/abi.cuh:109-121): host memory for the planners, device
+    memory for the launchers and kernels."""
+
+    _fields_ = [
+        ("rank", c_int),
+        ("reserved", c_int),
+        ("offset", c_longlong),
+        ("extents", c_void_p),
+        ("strides", c_void_p),
+    ]
+
+
 class CTransposeConfig(ctypes.Structure):
     """t4a_cuda_transpose_config: 16 bytes (reference abi.cuh:239-245)."""
 
@@ -65,6 +79,7 @@ class CReductionPlan(ctypes.Structure):
 assert ctypes.sizeof(CLayout) == 144 and ctypes.alignment(CLayout) == 8
 assert CLayout.offset.offset == 8 and CLayout.extents.offset == 16 and CLayout.strides.offset == 80
 assert ctypes.sizeof(CTransposeConfig) == 16
+assert ctypes.sizeof(CLayoutAny) == 32 and CLayoutAny.extents.offset == 16
 
 # Every C symbol declared in include/t4a/t4a.h, with its ctypes signature.
 SIGNATURES = {
@@ -115,6 +130,34 @@ SIGNATURES = {
     "t4a_hip_reduce_partials": (c_int, [c_void_p, c_void_p, c_int, c_int, POINTER(CLayout),
                                         POINTER(CLayout), c_int, c_longlong, c_longlong,
                                         c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_plan_materialize_strided_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                                 POINTER(CLaunch)]),
+    "t4a_plan_strided_to_strided_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                                POINTER(CLayoutAny), c_longlong,
+                                                POINTER(CLaunch)]),
+    "t4a_plan_reduce_any": (c_int, [c_int, c_int, c_int, POINTER(CLayoutAny), c_longlong,
+                                    POINTER(CLayoutAny), c_longlong, c_uint, c_uint,
+                                    POINTER(CLaunch)]),
+    "t4a_plan_reduce_partials_any": (c_int, [c_int, c_int, POINTER(CLayoutAny), c_longlong,
+                                             POINTER(CLayoutAny), c_longlong, c_uint, CSplit,
+                                             c_uint, POINTER(CLaunch)]),
+    "t4a_plan_reduction_any": (c_int, [c_int, c_int, POINTER(CLayoutAny), c_longlong,
+                                       POINTER(CLayoutAny), c_longlong, c_uint, c_uint,
+                                       POINTER(CReductionPlan)]),
+    "t4a_reduction_partials_layout_any": (c_int, [POINTER(CLayoutAny), c_uint, c_longlong,
+                                                  POINTER(c_longlong), POINTER(c_longlong)]),
+    "t4a_hip_materialize_strided_any": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayoutAny),
+                                                c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_strided_to_strided_any": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayoutAny),
+                                               POINTER(CLayoutAny), c_longlong,
+                                               POINTER(CLaunch), c_void_p]),
+    "t4a_hip_reduce_any": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, POINTER(CLayoutAny),
+                                   POINTER(CLayoutAny), c_int, c_longlong, POINTER(CLaunch),
+                                   c_void_p]),
+    "t4a_hip_reduce_partials_any": (c_int, [c_void_p, c_void_p, c_int, c_int,
+                                            POINTER(CLayoutAny), POINTER(CLayoutAny), c_int,
+                                            c_longlong, c_longlong, c_longlong,
+                                            POINTER(CLaunch), c_void_p]),
     "t4a_hip_reduction": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int,
                                   POINTER(CLayout), POINTER(CLayout), c_int, c_longlong,
                                   POINTER(CReductionPlan), c_void_p]),

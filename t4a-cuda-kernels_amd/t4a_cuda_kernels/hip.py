@@ -84,6 +84,44 @@ def reduce_partials(partials, inp, dtype: DType, op: ReduceOp, partials_layout: 
         _stream(stream)))
 
 
+# ---- general-rank twins: layouts are t4a_cuda_layout_any structs whose arrays
+# live in device memory (WideLayout.device_c over device copies of
+# WideLayout.extents / .strides), ordered before the launch on `stream`.
+
+def materialize_strided_any(dst, src, dtype: DType, src_layout, length: int, launch: Launch,
+                            stream=None) -> None:
+    """Reference t4a_cuda_materialize_strided_any (cuda/src/movement.cu:620-626)."""
+    _check(_lib.load().t4a_hip_materialize_strided_any(
+        _ptr(dst), _ptr(src), int(dtype), byref(src_layout), length, byref(launch.to_c()),
+        _stream(stream)))
+
+
+def strided_to_strided_any(dst, src, dtype: DType, src_layout, dst_layout, length: int,
+                           launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_strided_to_strided_any (cuda/src/movement.cu:638-646)."""
+    _check(_lib.load().t4a_hip_strided_to_strided_any(
+        _ptr(dst), _ptr(src), int(dtype), byref(src_layout), byref(dst_layout), length,
+        byref(launch.to_c()), _stream(stream)))
+
+
+def reduce_any(out, inp, dtype: DType, op: ReduceOp, strategy: ReduceStrategy, out_layout,
+               in_layout, axis: int, output_len: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_reduce_any (cuda/src/reduce.cu:854-900)."""
+    _check(_lib.load().t4a_hip_reduce_any(
+        _ptr(out), _ptr(inp), int(dtype), int(op), int(strategy), byref(out_layout),
+        byref(in_layout), axis, output_len, byref(launch.to_c()), _stream(stream)))
+
+
+def reduce_partials_any(partials, inp, dtype: DType, op: ReduceOp, partials_layout, in_layout,
+                        axis: int, output_len: int, splits: int, chunk_len: int,
+                        launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_reduce_partials_any (cuda/src/reduce.cu:902-940)."""
+    _check(_lib.load().t4a_hip_reduce_partials_any(
+        _ptr(partials), _ptr(inp), int(dtype), int(op), byref(partials_layout),
+        byref(in_layout), axis, output_len, splits, chunk_len, byref(launch.to_c()),
+        _stream(stream)))
+
+
 def enqueue_reduction(plan: ReductionPlan, out, inp, partials, dtype: DType, op: ReduceOp,
                       out_layout: Layout, in_layout: Layout, axis: int, output_len: int,
                       stream=None) -> Optional[Layout]:

@@ -16,7 +16,8 @@ HEADER = REPO / "include" / "t4a" / "t4a.h"
 ABI_HEADER = REPO / "include" / "t4a" / "abi.h"
 
 # The reference's kernel entries this library exports under the same names
-# (reference cuda/src/movement.cu:528-610, cuda/src/reduce.cu:765-852).
+# (reference cuda/src/movement.cu:528-646, cuda/src/reduce.cu:765-940), the
+# general-rank `_any` twins included.
 KERNEL_SYMBOLS = [
     "t4a_cuda_copy_exact",
     "t4a_cuda_materialize_strided",
@@ -24,6 +25,10 @@ KERNEL_SYMBOLS = [
     "t4a_cuda_tiled_transpose",
     "t4a_cuda_reduce",
     "t4a_cuda_reduce_partials",
+    "t4a_cuda_materialize_strided_any",
+    "t4a_cuda_strided_to_strided_any",
+    "t4a_cuda_reduce_any",
+    "t4a_cuda_reduce_partials_any",
 ]
 
 
@@ -53,8 +58,8 @@ def test_code_objects_export_the_reference_kernel_entries():
     """The gfx950 code objects a module-loading caller finds kernels in by name."""
     readelf = Path("/opt/rocm/llvm/bin/llvm-readelf")
     pkg = Path(_lib.LIB_PATH).parent
-    wanted = {"t4a_movement.gfx950.hsaco": KERNEL_SYMBOLS[:4],
-              "t4a_reduce.gfx950.hsaco": KERNEL_SYMBOLS[4:]}
+    wanted = {"t4a_movement.gfx950.hsaco": [n for n in KERNEL_SYMBOLS if "reduce" not in n],
+              "t4a_reduce.gfx950.hsaco": [n for n in KERNEL_SYMBOLS if "reduce" in n]}
     for name, symbols in wanted.items():
         path = pkg / name
         assert path.exists(), f"{name} not built"
