@@ -8,6 +8,7 @@
  *
  *   t4a_cuda_layout            reference cuda/include/t4a/abi.cuh:47-57
  *   t4a_cuda_layout_any        reference cuda/include/t4a/abi.cuh:109-121
+ *   t4a_cuda_axis_values(_any) reference cuda/include/t4a/abi.cuh:74-79, 122-126
  *   t4a_cuda_transpose_config  reference cuda/include/t4a/abi.cuh:239-245
  *   t4a_cuda_dtype tags        reference cuda/include/t4a/abi.cuh:25-33
  *   reduce op / strategy tags  reference cuda/include/t4a/abi.cuh:59-71
@@ -76,6 +77,23 @@ typedef struct {
   const long long* strides;
 } t4a_cuda_layout_any;
 
+/* A per-axis value map (broadcast_in_dim's `dims`: values[src_axis] is the
+ * destination axis of input axis src_axis). 72 bytes, alignment 8: rank 0,
+ * reserved 4, values 8; unused slots zero. */
+typedef struct {
+  int rank;
+  int reserved;
+  long long values[T4A_CUDA_MAX_RANK];
+} t4a_cuda_axis_values;
+
+/* Its general-rank form: `rank` values by pointer (device memory for the
+ * kernels, host memory for the planners). 16 bytes, alignment 8. */
+typedef struct {
+  int rank;
+  int reserved;
+  const long long* values;
+} t4a_cuda_axis_values_any;
+
 typedef enum {
   T4A_CUDA_REDUCE_SUM = 0,
   T4A_CUDA_REDUCE_PROD = 1,
@@ -120,6 +138,11 @@ T4A_STATIC_ASSERT(T4A_ALIGNOF(t4a_cuda_layout_any) == 8, "t4a_cuda_layout_any al
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, offset) == 8, "t4a_cuda_layout_any.offset");
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, extents) == 16, "t4a_cuda_layout_any.extents");
 T4A_STATIC_ASSERT(offsetof(t4a_cuda_layout_any, strides) == 24, "t4a_cuda_layout_any.strides");
+T4A_STATIC_ASSERT(sizeof(t4a_cuda_axis_values) == 72, "t4a_cuda_axis_values size");
+T4A_STATIC_ASSERT(offsetof(t4a_cuda_axis_values, values) == 8, "t4a_cuda_axis_values.values");
+T4A_STATIC_ASSERT(sizeof(t4a_cuda_axis_values_any) == 16, "t4a_cuda_axis_values_any size");
+T4A_STATIC_ASSERT(offsetof(t4a_cuda_axis_values_any, values) == 8,
+                  "t4a_cuda_axis_values_any.values");
 T4A_STATIC_ASSERT(sizeof(t4a_cuda_transpose_config) == 16, "t4a_cuda_transpose_config size");
 T4A_STATIC_ASSERT(T4A_ALIGNOF(t4a_cuda_transpose_config) == 4,
                   "t4a_cuda_transpose_config alignment");

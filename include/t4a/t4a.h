@@ -129,6 +129,23 @@ int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long lon
 int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
                                 const t4a_cuda_layout* dst, long long dst_len,
                                 t4a_launch* launch);
+/* Reference plan_fill_zero (src/lib.rs:1601-1603). */
+int t4a_plan_fill_zero(int dtype, long long len, t4a_launch* launch);
+/* Reference plan_fill_zero_view (src/lib.rs:1605-1622). */
+int t4a_plan_fill_zero_view(int dtype, const t4a_cuda_layout* dst, long long dst_len,
+                            t4a_launch* launch);
+/* Reference plan_contiguous_to_view (src/lib.rs:1641-1658). */
+int t4a_plan_contiguous_to_view(int dtype, const t4a_cuda_layout* dst, long long dst_len,
+                                t4a_launch* launch);
+/* Reference plan_broadcast_in_dim (src/lib.rs:1484-1533): dims->values[i] is
+ * the destination axis of input axis i; dims->rank must be the input rank. */
+int t4a_plan_broadcast_in_dim(int dtype, const t4a_cuda_layout* out, long long out_len,
+                              const t4a_cuda_layout* in, long long in_len,
+                              const t4a_cuda_axis_values* dims, t4a_launch* launch);
+/* Reference plan_concatenate_copy (src/lib.rs:1535-1589). */
+int t4a_plan_concatenate_copy(int dtype, const t4a_cuda_layout* out, long long out_len,
+                              const t4a_cuda_layout* in, long long in_len, unsigned int axis,
+                              long long axis_offset, t4a_launch* launch);
 /* Reference TransposeConfig::new (src/lib.rs:471-491). */
 int t4a_transpose_config_new(int tile, int block_rows, int padding, int vector_width,
                              t4a_cuda_transpose_config* config);
@@ -178,6 +195,16 @@ int t4a_plan_reduce_partials_any(int dtype, int op, const t4a_cuda_layout_any* p
                                  long long partials_len, const t4a_cuda_layout_any* in_layout,
                                  long long in_len, unsigned int axis, t4a_split split,
                                  unsigned int plane_width, t4a_launch* launch);
+int t4a_plan_fill_zero_view_any(int dtype, const t4a_cuda_layout_any* dst, long long dst_len,
+                                t4a_launch* launch);
+int t4a_plan_contiguous_to_view_any(int dtype, const t4a_cuda_layout_any* dst,
+                                    long long dst_len, t4a_launch* launch);
+int t4a_plan_broadcast_in_dim_any(int dtype, const t4a_cuda_layout_any* out, long long out_len,
+                                  const t4a_cuda_layout_any* in, long long in_len,
+                                  const t4a_cuda_axis_values_any* dims, t4a_launch* launch);
+int t4a_plan_concatenate_copy_any(int dtype, const t4a_cuda_layout_any* out, long long out_len,
+                                  const t4a_cuda_layout_any* in, long long in_len,
+                                  unsigned int axis, long long axis_offset, t4a_launch* launch);
 /* Writes pass1 / pass2 variants as above. */
 int t4a_plan_reduction_any(int dtype, int op, const t4a_cuda_layout_any* out_layout,
                            long long out_len, const t4a_cuda_layout_any* in_layout,
@@ -214,6 +241,26 @@ int t4a_hip_strided_to_strided(void* dst, const void* src, int dtype,
                                const t4a_cuda_layout* src_layout,
                                const t4a_cuda_layout* dst_layout, long long len,
                                const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_fill_zero, cuda/src/movement.cu:514-518. */
+int t4a_hip_fill_zero(void* out, int dtype, long long len, const t4a_launch* launch,
+                      void* stream);
+/* Reference t4a_cuda_fill_zero_view, cuda/src/movement.cu:520-526. */
+int t4a_hip_fill_zero_view(void* out, int dtype, const t4a_cuda_layout* layout, long long len,
+                           const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_contiguous_to_view, cuda/src/movement.cu:544-551. */
+int t4a_hip_contiguous_to_view(void* dst, const void* src, int dtype,
+                               const t4a_cuda_layout* dst_layout, long long len,
+                               const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_broadcast_in_dim, cuda/src/movement.cu:648-656. */
+int t4a_hip_broadcast_in_dim(void* out, const void* in, int dtype,
+                             const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
+                             const t4a_cuda_axis_values* dims, long long out_len,
+                             const t4a_launch* launch, void* stream);
+/* Reference t4a_cuda_concatenate_copy, cuda/src/movement.cu:668-676. */
+int t4a_hip_concatenate_copy(void* out, const void* in, int dtype,
+                             const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
+                             int axis, long long axis_offset, long long in_len,
+                             const t4a_launch* launch, void* stream);
 /* Reference t4a_cuda_reduce, cuda/src/reduce.cu:765-768. */
 int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int strategy,
                    const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
@@ -237,6 +284,21 @@ int t4a_hip_strided_to_strided_any(void* dst, const void* src, int dtype,
                                    const t4a_cuda_layout_any* src_layout,
                                    const t4a_cuda_layout_any* dst_layout, long long len,
                                    const t4a_launch* launch, void* stream);
+int t4a_hip_fill_zero_view_any(void* out, int dtype, const t4a_cuda_layout_any* layout,
+                               long long len, const t4a_launch* launch, void* stream);
+int t4a_hip_contiguous_to_view_any(void* dst, const void* src, int dtype,
+                                   const t4a_cuda_layout_any* dst_layout, long long len,
+                                   const t4a_launch* launch, void* stream);
+int t4a_hip_broadcast_in_dim_any(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout_any* out_layout,
+                                 const t4a_cuda_layout_any* in_layout,
+                                 const t4a_cuda_axis_values_any* dims, long long out_len,
+                                 const t4a_launch* launch, void* stream);
+int t4a_hip_concatenate_copy_any(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout_any* out_layout,
+                                 const t4a_cuda_layout_any* in_layout, int axis,
+                                 long long axis_offset, long long in_len,
+                                 const t4a_launch* launch, void* stream);
 int t4a_hip_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
                        const t4a_cuda_layout_any* out_layout,
                        const t4a_cuda_layout_any* in_layout, int axis, long long output_len,

@@ -65,6 +65,78 @@ void t4a_oracle_strided_to_strided(void* dst, const void* src, int dtype,
   }
 }
 
+void t4a_oracle_fill_zero_view(void* out, int dtype, const t4a_cuda_layout* l, long long len) {
+  const int es = t4a_oracle_dtype_size(dtype);
+  if (es == 0) return;
+  unsigned char* o = (unsigned char*)out;
+  for (long long f = 0; f < len; ++f) {
+    const long long index = decode(f, l->rank, l->extents, l->strides, l->offset);
+    memset(o + index * es, 0, (size_t)es); /* every dtype's zero is all-zero bits */
+  }
+}
+
+void t4a_oracle_contiguous_to_view(void* dst, const void* src, int dtype,
+                                   const t4a_cuda_layout* l, long long len) {
+  const int es = t4a_oracle_dtype_size(dtype);
+  if (es == 0) return;
+  unsigned char* d = (unsigned char*)dst;
+  const unsigned char* s = (const unsigned char*)src;
+  for (long long f = 0; f < len; ++f) {
+    const long long index = decode(f, l->rank, l->extents, l->strides, l->offset);
+    memcpy(d + index * es, s + f * es, (size_t)es);
+  }
+}
+
+/* Coordinates of flat index `f` over a layout's extents, axis 0 first
+ * (reference cuda/src/movement.cu:397-408). */
+static void coords_of(long long f, const t4a_cuda_layout* l, long long* c) {
+  for (int axis = 0; axis < T4A_CUDA_MAX_RANK; ++axis) {
+    c[axis] = 0;
+    if (axis < l->rank) {
+      c[axis] = f % l->extents[axis];
+      f /= l->extents[axis];
+    }
+  }
+}
+
+void t4a_oracle_broadcast_in_dim(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout* ol, const t4a_cuda_layout* il,
+                                 const long long* dims, int dims_rank, long long out_len) {
+  const int es = t4a_oracle_dtype_size(dtype);
+  if (es == 0) return;
+  unsigned char* o = (unsigned char*)out;
+  const unsigned char* s = (const unsigned char*)in;
+  long long c[T4A_CUDA_MAX_RANK];
+  for (long long f = 0; f < out_len; ++f) {
+    coords_of(f, ol, c);
+    long long index = il->offset;
+    for (int i = 0; i < dims_rank; ++i) {
+      const long long coordinate = il->extents[i] == 1 ? 0 : c[dims[i]];
+      index += coordinate * il->strides[i];
+    }
+    memcpy(o + f * es, s + index * es, (size_t)es); /* the destination is compact */
+  }
+}
+
+void t4a_oracle_concatenate_copy(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout* ol, const t4a_cuda_layout* il, int axis,
+                                 long long axis_offset, long long in_len) {
+  const int es = t4a_oracle_dtype_size(dtype);
+  if (es == 0) return;
+  unsigned char* o = (unsigned char*)out;
+  const unsigned char* s = (const unsigned char*)in;
+  long long c[T4A_CUDA_MAX_RANK];
+  for (long long f = 0; f < in_len; ++f) {
+    coords_of(f, il, c);
+    long long index = ol->offset;
+    for (int k = 0; k < ol->rank; ++k) {
+      const long long coordinate = k == axis ? c[k] + axis_offset : c[k];
+      index += coordinate * ol->strides[k];
+    }
+    memcpy(o + index * es, s + f * es, (size_t)es); /* the source is compact */
+  }
+}
+
 void t4a_oracle_tiled_transpose(void* dst, const void* src, int dtype, long long src_offset,
                                 long long batch_stride, long long m, long long n,
                                 long long batches) {

@@ -37,6 +37,31 @@ void t4a_oracle_strided_to_strided(void* dst, const void* src, int dtype,
                                    const t4a_cuda_layout* src_layout,
                                    const t4a_cuda_layout* dst_layout, long long len);
 
+/* out[decode(f, layout)] = zero (all-zero bits) for f < len.
+ * Reference: cuda/src/movement.cu:79-96, abi.cuh:520-538 (t4a_cuda_zero). */
+void t4a_oracle_fill_zero_view(void* out, int dtype, const t4a_cuda_layout* layout,
+                               long long len);
+
+/* dst[decode(f, dst_layout)] = src[f]. Reference: cuda/src/movement.cu:113-125. */
+void t4a_oracle_contiguous_to_view(void* dst, const void* src, int dtype,
+                                   const t4a_cuda_layout* dst_layout, long long len);
+
+/* out[f] = in[in.offset + sum_i (in.extents[i] == 1 ? 0 : coord(f, dims[i])) *
+ * in.strides[i]], coordinates over the (compact) destination's extents.
+ * Reference: cuda/src/movement.cu:397-437. */
+void t4a_oracle_broadcast_in_dim(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout* out_layout,
+                                 const t4a_cuda_layout* in_layout, const long long* dims,
+                                 int dims_rank, long long out_len);
+
+/* out[out.offset + sum_k (coord(f, in) + (k == axis ? axis_offset : 0)) *
+ * out.strides[k]] = in[f] for the compact input. Reference:
+ * cuda/src/movement.cu:441-466. */
+void t4a_oracle_concatenate_copy(void* out, const void* in, int dtype,
+                                 const t4a_cuda_layout* out_layout,
+                                 const t4a_cuda_layout* in_layout, int axis,
+                                 long long axis_offset, long long in_len);
+
 /* dst[b*S + i + j*M] = src[src_offset + b*S + i*N + j], S = M*N.
  * Reference: docs/abi/c-kernel-abi.md:151-159, tests/gpu_kernels.rs:330-339. */
 void t4a_oracle_tiled_transpose(void* dst, const void* src, int dtype, long long src_offset,

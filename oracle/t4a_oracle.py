@@ -39,10 +39,21 @@ def load() -> ctypes.CDLL:
                                                    c_longlong, c_longlong]
         lib.t4a_oracle_reduce_f64.argtypes = [POINTER(c_double), c_void_p, c_int, c_int,
                                               c_void_p, c_int, c_longlong]
+        lib.t4a_oracle_fill_zero_view.argtypes = [c_void_p, c_int, c_void_p, c_longlong]
+        lib.t4a_oracle_contiguous_to_view.argtypes = [c_void_p, c_void_p, c_int, c_void_p,
+                                                      c_longlong]
+        lib.t4a_oracle_broadcast_in_dim.argtypes = [c_void_p, c_void_p, c_int, c_void_p,
+                                                    c_void_p, POINTER(c_longlong), c_int,
+                                                    c_longlong]
+        lib.t4a_oracle_concatenate_copy.argtypes = [c_void_p, c_void_p, c_int, c_void_p,
+                                                    c_void_p, c_int, c_longlong, c_longlong]
         lib.t4a_oracle_fnv1a64.argtypes = [c_void_p, ctypes.c_ulonglong]
         lib.t4a_oracle_fnv1a64.restype = ctypes.c_ulonglong
         lib.t4a_oracle_dtype_size.argtypes = [c_int]
         lib.t4a_oracle_dtype_size.restype = c_int
+        for name in ("t4a_oracle_fill_zero_view", "t4a_oracle_contiguous_to_view",
+                     "t4a_oracle_broadcast_in_dim", "t4a_oracle_concatenate_copy"):
+            getattr(lib, name).restype = None
         for name in ("t4a_oracle_materialize_strided", "t4a_oracle_strided_to_strided",
                      "t4a_oracle_tiled_transpose", "t4a_oracle_reduce",
                      "t4a_oracle_reduce_partials", "t4a_oracle_reduce_f64"):
@@ -70,6 +81,28 @@ def strided_to_strided(dst: np.ndarray, src: np.ndarray, dtype: int, src_layout,
                        length: int) -> None:
     load().t4a_oracle_strided_to_strided(_p(dst), _p(src), int(dtype), _l(src_layout),
                                          _l(dst_layout), length)
+
+
+def fill_zero_view(out: np.ndarray, dtype: int, layout, length: int) -> None:
+    load().t4a_oracle_fill_zero_view(_p(out), int(dtype), _l(layout), length)
+
+
+def contiguous_to_view(dst: np.ndarray, src: np.ndarray, dtype: int, dst_layout,
+                       length: int) -> None:
+    load().t4a_oracle_contiguous_to_view(_p(dst), _p(src), int(dtype), _l(dst_layout), length)
+
+
+def broadcast_in_dim(out: np.ndarray, inp: np.ndarray, dtype: int, out_layout, in_layout,
+                     dims, out_len: int) -> None:
+    d = (c_longlong * max(len(dims), 1))(*dims)
+    load().t4a_oracle_broadcast_in_dim(_p(out), _p(inp), int(dtype), _l(out_layout),
+                                       _l(in_layout), d, len(dims), out_len)
+
+
+def concatenate_copy(out: np.ndarray, inp: np.ndarray, dtype: int, out_layout, in_layout,
+                     axis: int, axis_offset: int, in_len: int) -> None:
+    load().t4a_oracle_concatenate_copy(_p(out), _p(inp), int(dtype), _l(out_layout),
+                                       _l(in_layout), axis, axis_offset, in_len)
 
 
 def tiled_transpose(dst: np.ndarray, src: np.ndarray, dtype: int, src_offset: int,

@@ -170,22 +170,37 @@ T4A_HD int move_chain_contains(const int* dims, int count, int dim) {
 
 // Fused movement geometry of any rank: every axis of extent 1 dropped, and an
 // axis whose source and destination strides both continue the previous kept
-// axis's span merged into it (axis 0 first). `ds == nullptr` means the compact
-// destination of materialize_strided (strides by the running extent product).
-// Writes at most `cap` fused axes to fe / fs / fd and returns their count, or
-// -1 when more remain. With no extent 0 every fused axis has extent >= 2, so a
-// layout of fewer than 2^63 elements fuses to at most 62 axes.
+// axis's span merged into it (axis 0 first). `src(k)` / `dst(k)` give axis k's
+// strides (called once per axis, in axis order). Writes at most `cap` fused
+// axes to fe / fs / fd and returns their count, or -1 when more remain. With
+// no extent 0 every fused axis has extent >= 2, so a layout of fewer than 2^63
+// elements fuses to at most 62 axes.
 constexpr int kMaxFusedDims = 64;
 
-T4A_HD int fuse_move(int rank, const long long* ext, const long long* ss, const long long* ds,
-                     long long* fe, long long* fs, long long* fd, int cap) {
+// The element count a movement may touch: `len` (the caller's count) capped at
+// the product of the `n` extents, so a count past the layout's elements never
+// walks an axis past its extent. An extent <= 0 leaves nothing.
+T4A_HD long long clamp_count(int n, const long long* ext, long long len) {
+  if (len <= 0) return 0;
+  for (int k = 0; k < n; ++k) {
+    if (ext[k] <= 0) return 0;
+  }
+  long long c = 1;
+  for (int k = 0; k < n; ++k) {
+    if (c > len / ext[k]) return len;
+    c *= ext[k];
+  }
+  return c < len ? c : len;
+}
+
+template <typename SrcStride, typename DstStride>
+T4A_HD int fuse_move_by(int rank, const long long* ext, SrcStride src, DstStride dst,
+                        long long* fe, long long* fs, long long* fd, int cap) {
   int n = 0;
-  unsigned long long compact = 1;
   for (int k = 0; k < rank; ++k) {
     const long long e = ext[k];
-    const long long s = ss[k];
-    const long long d = ds ? ds[k] : static_cast<long long>(compact);
-    compact *= static_cast<unsigned long long>(e);
+    const long long s = src(k);
+    const long long d = dst(k);
     if (e == 1) continue;
     if (n > 0 && s == fs[n - 1] * fe[n - 1] && d == fd[n - 1] * fe[n - 1]) {
       fe[n - 1] *= e;
@@ -198,6 +213,55 @@ T4A_HD int fuse_move(int rank, const long long* ext, const long long* ss, const 
     ++n;
   }
   return n;
+}
+
+// Strides of a compact layout over `ext`, axis by axis in order (the running
+// extent product; a stateful functor for fuse_move_by).
+struct CompactStrides {
+  const long long* ext;
+  unsigned long long next;
+  T4A_HD long long operator()(int k) {
+    const long long s = static_cast<long long>(next);
+    next *= static_cast<unsigned long long>(ext[k]);
+    return s;
+  }
+};
+
+// Array strides, or (null) those of the compact layout over `ext`.
+struct StridesOf {
+  const long long* strides;
+  CompactStrides compact;
+  T4A_HD long long operator()(int k) { return strides ? strides[k] : compact(k); }
+};
+
+T4A_HD StridesOf strides_of(const long long* strides, const long long* ext) {
+  return StridesOf{strides, CompactStrides{ext, 1}};
+}
+
+// broadcast_in_dim's source seen over the destination's axes (reference
+// cuda/src/movement.cu:409-434): destination axis k reads input axis i where
+// dims[i] = k with that axis's stride, or stride 0 (broadcast) when no input
+// axis maps to k or the input extent there is one.
+struct BroadcastStrides {
+  const long long* dims;
+  int dims_rank;
+  const long long* in_ext;
+  const long long* in_st;
+  T4A_HD long long operator()(int k) const {
+    for (int i = 0; i < dims_rank; ++i) {
+      if (dims[i] == k) return in_ext[i] == 1 ? 0 : in_st[i];
+    }
+    return 0;
+  }
+};
+
+// Array strides, or the compact layout's when `strides` is null.
+T4A_HD int fuse_move(int rank, const long long* ext, const long long* ss, const long long* ds,
+                     long long* fe, long long* fs, long long* fd, int cap) {
+  CompactStrides cs{ext, 1}, cd{ext, 1};
+  return fuse_move_by(
+      rank, ext, [&](int k) { return ss ? ss[k] : cs(k); },
+      [&](int k) { return ds ? ds[k] : cd(k); }, fe, fs, fd, cap);
 }
 
 // `dst_strides == nullptr` means the compact destination of materialize_strided.
@@ -215,9 +279,11 @@ T4A_HD void move_plan_view(MovePlan* p, int rank, long long src_offset, const lo
   p->na = p->nb = p->nbatch = 0;
   p->tiles = 0;
   p->row_dim = -1;
-  if (len <= 0) return;
   if (rank < 0) rank = 0;
   if (rank > kMaxDims) rank = kMaxDims;
+  len = clamp_count(rank, src_ext, len);
+  p->len = len;
+  if (len <= 0) return;
   long long compact = 1;
   for (int k = 0; k < rank; ++k) {
     const long long e = src_ext[k];
@@ -381,6 +447,78 @@ T4A_HD void move_plan(MovePlan* p, const t4a_cuda_layout& src, const long long* 
                       long long dst_offset, long long len, int esize) {
   move_plan_view(p, src.rank, src.offset, src.extents, src.strides, dst_strides, dst_offset, len,
                  esize);
+}
+
+// The plan of a move over derived geometry (the general-rank entries'
+// in-kernel planning; host use: its arrays are 1.5 KiB of stack). False when
+// more than kMaxDims fused axes remain (the general twins decode those per
+// element).
+template <typename SrcStride, typename DstStride>
+T4A_HD bool move_plan_by(MovePlan* p, int rank, const long long* ext, SrcStride src,
+                         long long src_offset, DstStride dst, long long dst_offset, long long len,
+                         int esize) {
+  long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
+  const int n = len > 0 ? fuse_move_by(rank, ext, src, dst, fe, fs, fd, kMaxFusedDims) : 0;
+  if (n < 0 || n > kMaxDims) return false;
+  move_plan_view(p, n, src_offset, fe, fs, fd, dst_offset, len, esize);
+  return true;
+}
+
+// fill_zero_view: the view's fused axes (fuse_move with the view's strides on
+// both sides), the stride-1 axis, if any, moved first so that consecutive flat
+// indices are consecutive addresses (every element gets the same zero, so the
+// order of the walk is free). At most kMaxDims axes; the general-rank entry
+// decodes wider views itself.
+struct FillPlan {
+  int n;
+  long long ext[kMaxDims];
+  long long st[kMaxDims];
+  long long offset;
+  long long len;
+  bool narrow;  // len below 2^32: 32-bit quotients
+};
+
+T4A_HD bool fill_plan(FillPlan* p, int n, const long long* fe, const long long* fs,
+                      long long offset, long long len) {
+  if (n < 0 || n > kMaxDims) return false;
+  len = clamp_count(n, fe, len);
+  p->n = n;
+  p->offset = offset;
+  p->len = len;
+  p->narrow = len >= 0 && len < (1ll << 32);
+  int unit = -1;
+  for (int k = 0; k < n; ++k) {
+    if (fs[k] == 1 && unit < 0) unit = k;
+  }
+  int w = 0;
+  if (unit >= 0) {
+    p->ext[w] = fe[unit];
+    p->st[w] = fs[unit];
+    ++w;
+  }
+  for (int k = 0; k < n; ++k) {
+    if (k == unit) continue;
+    p->ext[w] = fe[k];
+    p->st[w] = fs[k];
+    ++w;
+  }
+  for (int k = n; k < kMaxDims; ++k) {
+    p->ext[k] = 1;
+    p->st[k] = 0;
+  }
+  return true;
+}
+
+// Whether V consecutive flat indices are V consecutive, V-aligned elements:
+// the first axis contiguous with an extent that V divides, and the offset and
+// every other stride multiples of V (the pointer's alignment is the caller's).
+T4A_HD bool fill_vectorizable(const FillPlan& p, int v) {
+  if (v <= 1 || p.n == 0 || p.st[0] != 1 || p.ext[0] % v != 0 || p.offset % v != 0)
+    return false;
+  for (int k = 1; k < p.n; ++k) {
+    if (p.st[k] % v != 0) return false;
+  }
+  return true;
 }
 
 // The one-tile-per-block form of a TILED plan: a block moves tile blockIdx.x

@@ -651,27 +651,27 @@ __device__ __forceinline__ void move_elements_wide(void* dst, const void* src, i
   }
 }
 
-// `dst_layout == nullptr`: the compact destination of materialize_strided.
-// Ranks that differ, or a negative rank, do no work.
-__device__ __forceinline__ void move_entry_any(void* dst, const void* src, int dtype,
-                                               const t4a_cuda_layout_any& src_layout,
-                                               const t4a_cuda_layout_any* dst_layout,
-                                               long long len) {
+// A move over derived geometry, planned by thread 0 in LDS: `rank` axes of
+// extents `ext` (device memory, read once), source strides src(k) from
+// `src_offset`, destination strides dst(k) from `dst_offset` (callables, axis
+// by axis in order). `ok` false does no work.
+template <typename SrcStride, typename DstStride>
+__device__ __forceinline__ void move_entry_by(void* dst, const void* src, int dtype, bool ok,
+                                              int rank, const long long* ext, SrcStride src_st,
+                                              long long src_offset, DstStride dst_st,
+                                              long long dst_offset, long long len) {
   const int es = dtype_size(dtype);
-  if (es == 0 || len <= 0) return;
+  if (es == 0 || len <= 0 || !ok || rank < 0) return;
   __shared__ MovePlan plan;
   __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
   __shared__ int fused;
+  __shared__ long long count;
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
-  const long long dst_offset = dst_layout ? dst_layout->offset : 0;
   if (threadIdx.x == 0) {
-    fused = -1;
-    if (src_layout.rank >= 0 && (dst_layout == nullptr || dst_layout->rank == src_layout.rank)) {
-      fused = fuse_move(src_layout.rank, src_layout.extents, src_layout.strides,
-                        dst_layout ? dst_layout->strides : nullptr, fe, fs, fd, kMaxFusedDims);
-      if (fused >= 0 && fused <= kMaxDims)
-        move_plan_view(&plan, fused, src_layout.offset, fe, fs, fd, dst_offset, len, es);
-    }
+    fused = fuse_move_by(rank, ext, src_st, dst_st, fe, fs, fd, kMaxFusedDims);
+    count = fused >= 0 ? clamp_count(fused, fe, len) : 0;
+    if (fused >= 0 && fused <= kMaxDims)
+      move_plan_view(&plan, fused, src_offset, fe, fs, fd, dst_offset, len, es);
   }
   __syncthreads();
   if (fused < 0) return;
@@ -680,7 +680,7 @@ __device__ __forceinline__ void move_entry_any(void* dst, const void* src, int d
     if (fused <= kMaxDims) {
       move_dispatch<P>(dst, src, plan, lds);
     } else {
-      move_elements_wide<P>(dst, src, fused, fe, fs, fd, src_layout.offset, dst_offset, len);
+      move_elements_wide<P>(dst, src, fused, fe, fs, fd, src_offset, dst_offset, count);
     }
   };
   switch (es) {
@@ -690,6 +690,19 @@ __device__ __forceinline__ void move_entry_any(void* dst, const void* src, int d
     case 16: run(static_cast<Elem16*>(nullptr)); break;
     default: break;
   }
+}
+
+// `dst_layout == nullptr`: the compact destination of materialize_strided.
+// Ranks that differ do no work.
+__device__ __forceinline__ void move_entry_any(void* dst, const void* src, int dtype,
+                                               const t4a_cuda_layout_any& src_layout,
+                                               const t4a_cuda_layout_any* dst_layout,
+                                               long long len) {
+  const bool ok = dst_layout == nullptr || dst_layout->rank == src_layout.rank;
+  move_entry_by(dst, src, dtype, ok, src_layout.rank, src_layout.extents,
+                strides_of(src_layout.strides, src_layout.extents), src_layout.offset,
+                strides_of(dst_layout ? dst_layout->strides : nullptr, src_layout.extents),
+                dst_layout ? dst_layout->offset : 0, len);
 }
 
 // ---- copy_exact -----------------------------------------------------------------------
@@ -737,6 +750,126 @@ __device__ __forceinline__ void copy_body(void* dst, const void* src, long long 
                        blocks);
 }
 
+// ---- fill_zero / fill_zero_view -------------------------------------------------------
+// Every element type's zero is all-zero bits (reference t4a_cuda_zero,
+// cuda/include/t4a/abi.cuh:520-538: 0, +0.0, {+0.0, +0.0}). fill_zero writes
+// len contiguous elements as the copy streams them: one non-temporal 16-byte
+// vector per thread when the buffer is 16-byte aligned, element by element
+// after the last whole vector and otherwise (reference movement.cu:70-76).
+template <typename P, int BS>
+__device__ __forceinline__ void fill_body(void* out, long long len, unsigned int blocks) {
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(blocks) * bs;
+  long long first = 0;
+  if ((reinterpret_cast<uintptr_t>(out) & 15) == 0 && sizeof(P) <= 16) {
+    const long long vectors = len * static_cast<long long>(sizeof(P)) / 16;
+    Bits128* o = static_cast<Bits128*>(out);
+    const Vec<Bits128, 1> zero{};
+    for (long long i = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; i < vectors;
+         i += gstride)
+      nt_store<Bits128, 1>(o + i, zero);
+    first = vectors * 16 / static_cast<long long>(sizeof(P));
+  }
+  P* o = static_cast<P*>(out);
+  for (long long i = first + static_cast<long long>(blockIdx.x) * bs + threadIdx.x; i < len;
+       i += gstride)
+    o[i] = P{};
+}
+
+// fill_zero_view over a FillPlan: V flat indices per thread, stored as one
+// vector when fill_vectorizable (reference movement.cu:78-96 zeroes one element
+// per thread at its decoded address).
+template <typename P, int V>
+__device__ __forceinline__ void fill_view_body(void* out, const FillPlan& fp) {
+  P* o = static_cast<P*>(out) + fp.offset;
+  const long long units = fp.len / V;
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  const Vec<P, V> zero{};
+  for (long long u = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; u < units;
+       u += gstride) {
+    long long off = 0;
+    if (fp.narrow) {
+      unsigned int r = static_cast<unsigned int>(u * V);
+#pragma unroll
+      for (int k = 0; k < kMaxDims; ++k) {
+        if (k >= fp.n) break;
+        const unsigned int e = static_cast<unsigned int>(fp.ext[k]);
+        off += static_cast<long long>(r % e) * fp.st[k];
+        r /= e;
+      }
+    } else {
+      long long r = u * V;
+#pragma unroll
+      for (int k = 0; k < kMaxDims; ++k) {
+        if (k >= fp.n) break;
+        off += (r % fp.ext[k]) * fp.st[k];
+        r /= fp.ext[k];
+      }
+    }
+    nt_store<P, V>(o + off, zero);
+  }
+}
+
+// A fused view wider than kMaxDims axes (the general-rank entry): one element
+// per thread, decoded over the LDS-resident axes.
+template <typename P>
+__device__ __forceinline__ void fill_view_wide(void* out, int n, const long long* fe,
+                                               const long long* fs, long long offset,
+                                               long long len) {
+  P* o = static_cast<P*>(out);
+  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < len;
+       f += gstride) {
+    long long rest = f;
+    long long off = offset;
+    for (int k = 0; k < n; ++k) {
+      off += (rest % fe[k]) * fs[k];
+      rest /= fe[k];
+    }
+    o[off] = P{};
+  }
+}
+
+// The entries' fill: thread 0 fuses the view (any rank, arrays read once)
+// into LDS and builds the plan; 16-byte stores where the plan and pointer
+// allow.
+__device__ __forceinline__ void fill_view_entry(void* out, int dtype, int rank, long long offset,
+                                                const long long* ext, const long long* st,
+                                                long long len) {
+  const int es = dtype_size(dtype);
+  if (es == 0 || len <= 0 || rank < 0) return;
+  __shared__ FillPlan plan;
+  __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
+  __shared__ int fused;
+  __shared__ long long count;
+  if (threadIdx.x == 0) {
+    fused = fuse_move(rank, ext, st, st, fe, fs, fd, kMaxFusedDims);
+    count = fused >= 0 ? clamp_count(fused, fe, len) : 0;
+    if (fused >= 0 && fused <= kMaxDims) fill_plan(&plan, fused, fe, fs, offset, len);
+  }
+  __syncthreads();
+  if (fused < 0) return;
+  auto run = [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
+    if (fused > kMaxDims) {
+      fill_view_wide<P>(out, fused, fe, fs, offset, count);
+    } else if (V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+               fill_vectorizable(plan, V)) {
+      fill_view_body<P, V>(out, plan);
+    } else {
+      fill_view_body<P, 1>(out, plan);
+    }
+  };
+  switch (es) {
+    case 1: run(static_cast<uint8_t*>(nullptr)); break;
+    case 4: run(static_cast<uint32_t*>(nullptr)); break;
+    case 8: run(static_cast<unsigned long long*>(nullptr)); break;
+    case 16: run(static_cast<Elem16*>(nullptr)); break;
+    default: break;
+  }
+}
+
 // ---- kernels the launchers use: one per payload width, the plan computed on
 // the host and passed by value. ----
 
@@ -760,6 +893,17 @@ __global__ void __launch_bounds__(256)
     move_tiled_kernel(void* dst, const void* src, MovePlan plan) {
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
   move_tiled_as<P, VL, VS>(dst, src, plan, lds);
+}
+
+template <typename P, int BS>
+__global__ void __launch_bounds__(256)
+    fill_kernel(void* out, long long len, unsigned int blocks) {
+  fill_body<P, BS>(out, len, blocks);
+}
+
+template <typename P, int V>
+__global__ void __launch_bounds__(256) fill_view_kernel(void* out, FillPlan fp) {
+  fill_view_body<P, V>(out, fp);
 }
 
 template <typename P, int VL, int VS, int LA, int LB>
@@ -849,6 +993,108 @@ extern "C" __global__ void __launch_bounds__(256)
                                     t4a_cuda_layout_any src_layout,
                                     t4a_cuda_layout_any dst_layout, long long len) {
   t4a::move_entry_any(dst, src, dtype, src_layout, &dst_layout, len);
+}
+
+// ---- the rest of the reference movement entries (movement.cu:514-551, 612-685) ----------
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_fill_zero(void* out, int dtype, long long len) {
+  switch (t4a::dtype_size(dtype)) {
+    case 1: t4a::fill_body<uint8_t, 0>(out, len, gridDim.x); break;
+    case 4: t4a::fill_body<uint32_t, 0>(out, len, gridDim.x); break;
+    case 8: t4a::fill_body<unsigned long long, 0>(out, len, gridDim.x); break;
+    case 16: t4a::fill_body<t4a::Elem16, 0>(out, len, gridDim.x); break;
+    default: break;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_fill_zero_view(void* out, int dtype, t4a_cuda_layout layout, long long len) {
+  t4a::fill_view_entry(out, dtype, layout.rank <= t4a::kMaxDims ? layout.rank : -1,
+                       layout.offset, layout.extents, layout.strides, len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_fill_zero_view_any(void* out, int dtype, t4a_cuda_layout_any layout,
+                                long long len) {
+  t4a::fill_view_entry(out, dtype, layout.rank, layout.offset, layout.extents, layout.strides,
+                       len);
+}
+
+// contiguous_to_view: dst[decode(f, dst_layout)] = src[f] (reference
+// movement.cu:112-125): a move from the compact layout over the view's extents.
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_contiguous_to_view(void* dst, const void* src, int dtype,
+                                t4a_cuda_layout dst_layout, long long len) {
+  const bool ok = dst_layout.rank >= 0 && dst_layout.rank <= t4a::kMaxDims;
+  t4a::move_entry_by(dst, src, dtype, ok, dst_layout.rank, dst_layout.extents,
+                     t4a::strides_of(nullptr, dst_layout.extents), 0,
+                     t4a::strides_of(dst_layout.strides, dst_layout.extents), dst_layout.offset,
+                     len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_contiguous_to_view_any(void* dst, const void* src, int dtype,
+                                    t4a_cuda_layout_any dst_layout, long long len) {
+  t4a::move_entry_by(dst, src, dtype, true, dst_layout.rank, dst_layout.extents,
+                     t4a::strides_of(nullptr, dst_layout.extents), 0,
+                     t4a::strides_of(dst_layout.strides, dst_layout.extents), dst_layout.offset,
+                     len);
+}
+
+// broadcast_in_dim: out[f] = in[sum over input axes i of coordinate(f, dims[i])
+// * in.strides[i], coordinate 0 where the input extent is one] into a compact
+// destination (reference movement.cu:409-434): a move whose source has the
+// destination's extents and stride 0 on broadcast axes.
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_broadcast_in_dim(void* out, const void* in, int dtype, t4a_cuda_layout out_layout,
+                              t4a_cuda_layout in_layout, t4a_cuda_axis_values dims,
+                              long long out_len) {
+  const bool ok = out_layout.rank >= 0 && out_layout.rank <= t4a::kMaxDims && dims.rank >= 0 &&
+                  dims.rank <= t4a::kMaxDims;
+  t4a::move_entry_by(out, in, dtype, ok, out_layout.rank, out_layout.extents,
+                     t4a::BroadcastStrides{dims.values, dims.rank, in_layout.extents,
+                                           in_layout.strides},
+                     in_layout.offset, t4a::strides_of(nullptr, out_layout.extents), 0, out_len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_broadcast_in_dim_any(void* out, const void* in, int dtype,
+                                  t4a_cuda_layout_any out_layout, t4a_cuda_layout_any in_layout,
+                                  t4a_cuda_axis_values_any dims, long long out_len) {
+  t4a::move_entry_by(out, in, dtype, dims.rank >= 0, out_layout.rank, out_layout.extents,
+                     t4a::BroadcastStrides{dims.values, dims.rank, in_layout.extents,
+                                           in_layout.strides},
+                     in_layout.offset, t4a::strides_of(nullptr, out_layout.extents), 0, out_len);
+}
+
+// concatenate_copy: out[decode(f shifted by axis_offset along axis, out)] =
+// in[f] for the compact input (reference movement.cu:436-465): a move from the
+// input into the destination's strides from the shifted origin.
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_concatenate_copy(void* out, const void* in, int dtype, t4a_cuda_layout out_layout,
+                              t4a_cuda_layout in_layout, int axis, long long axis_offset,
+                              long long in_len) {
+  const bool ok = in_layout.rank >= 0 && in_layout.rank <= t4a::kMaxDims &&
+                  out_layout.rank == in_layout.rank && axis >= 0 && axis < in_layout.rank;
+  const long long origin = ok ? out_layout.offset + axis_offset * out_layout.strides[axis] : 0;
+  t4a::move_entry_by(out, in, dtype, ok, in_layout.rank, in_layout.extents,
+                     t4a::strides_of(nullptr, in_layout.extents), 0,
+                     t4a::strides_of(out_layout.strides, in_layout.extents), origin, in_len);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    t4a_cuda_concatenate_copy_any(void* out, const void* in, int dtype,
+                                  t4a_cuda_layout_any out_layout, t4a_cuda_layout_any in_layout,
+                                  int axis, long long axis_offset, long long in_len) {
+  const bool ok = out_layout.rank == in_layout.rank && axis >= 0 && axis < in_layout.rank;
+  __shared__ long long origin;
+  if (threadIdx.x == 0)
+    origin = ok ? out_layout.offset + axis_offset * out_layout.strides[axis] : 0;
+  __syncthreads();
+  t4a::move_entry_by(out, in, dtype, ok, in_layout.rank, in_layout.extents,
+                     t4a::strides_of(nullptr, in_layout.extents), 0,
+                     t4a::strides_of(out_layout.strides, in_layout.extents), origin, in_len);
 }
 
 // ---- launchers -----------------------------------------------------------------------
@@ -1078,3 +1324,171 @@ extern "C" int t4a_hip_strided_to_strided_any(void* dst, const void* src, int dt
                      len);
   return status_of_last_launch();
 }
+
+// ---- the rest of the movement entries ---------------------------------------------------
+
+extern "C" int t4a_hip_fill_zero(void* out, int dtype, long long len, const t4a_launch* launch,
+                                 void* stream) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_payload(dtype, [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+      hipLaunchKernelGGL((t4a::fill_kernel<P, t4a::kBlock>), grid, block, 0, s, out, len,
+                         grid.x);
+    else
+      hipLaunchKernelGGL((t4a::fill_kernel<P, 0>), grid, block, 0, s, out, len, grid.x);
+    return status_of_last_launch();
+  });
+}
+
+extern "C" int t4a_hip_fill_zero_view(void* out, int dtype, const t4a_cuda_layout* layout,
+                                      long long len, const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  long long fe[t4a::kMaxFusedDims], fs[t4a::kMaxFusedDims], fd[t4a::kMaxFusedDims];
+  const int rank = layout->rank < 0 ? 0 : layout->rank > t4a::kMaxDims ? t4a::kMaxDims
+                                                                         : layout->rank;
+  const int n = t4a::fuse_move(rank, layout->extents, layout->strides, layout->strides, fe, fs,
+                               fd, t4a::kMaxFusedDims);
+  t4a::FillPlan fp;
+  if (!t4a::fill_plan(&fp, n, fe, fs, layout->offset, len)) return T4A_OK;
+  const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
+  const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
+  return with_payload(dtype, [&](auto* tag) {
+    using P = std::remove_pointer_t<decltype(tag)>;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    constexpr int V = t4a::tile_vector<P>();
+    if (V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && t4a::fill_vectorizable(fp, V))
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, V>), grid, block, 0, s, out, fp);
+    else
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, 1>), grid, block, 0, s, out, fp);
+    return status_of_last_launch();
+  });
+}
+
+// The copy-style entries: the same move machinery as strided_to_strided over
+// the geometry the entry implies (the planner derives the same plan).
+namespace {
+
+template <typename SrcStride, typename DstStride>
+int launch_derived(void* dst, const void* src, int dtype, int rank, const long long* ext,
+                   SrcStride src_st, long long src_offset, DstStride dst_st, long long dst_offset,
+                   long long len, const t4a_launch* launch, void* stream) {
+  if (rank < 0 || rank > t4a::kMaxDims) return T4A_OK;
+  t4a::MovePlan plan;
+  if (!t4a::move_plan_by(&plan, rank, ext, src_st, src_offset, dst_st, dst_offset, len,
+                         t4a::dtype_size(dtype)))
+    return T4A_OK;
+  return launch_move(dst, src, plan, launch, stream, dtype);
+}
+
+}  // namespace
+
+extern "C" int t4a_hip_contiguous_to_view(void* dst, const void* src, int dtype,
+                                          const t4a_cuda_layout* dst_layout, long long len,
+                                          const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || dst_layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (dst == nullptr || src == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  return launch_derived(dst, src, dtype, dst_layout->rank, dst_layout->extents,
+                        t4a::strides_of(nullptr, dst_layout->extents), 0,
+                        t4a::strides_of(dst_layout->strides, dst_layout->extents),
+                        dst_layout->offset, len, launch, stream);
+}
+
+extern "C" int t4a_hip_broadcast_in_dim(void* out, const void* in, int dtype,
+                                        const t4a_cuda_layout* out_layout,
+                                        const t4a_cuda_layout* in_layout,
+                                        const t4a_cuda_axis_values* dims, long long out_len,
+                                        const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr || dims == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (dims->rank < 0 || dims->rank > t4a::kMaxDims) return T4A_OK;
+  return launch_derived(out, in, dtype, out_layout->rank, out_layout->extents,
+                        t4a::BroadcastStrides{dims->values, dims->rank, in_layout->extents,
+                                              in_layout->strides},
+                        in_layout->offset, t4a::strides_of(nullptr, out_layout->extents), 0,
+                        out_len, launch, stream);
+}
+
+extern "C" int t4a_hip_concatenate_copy(void* out, const void* in, int dtype,
+                                        const t4a_cuda_layout* out_layout,
+                                        const t4a_cuda_layout* in_layout, int axis,
+                                        long long axis_offset, long long in_len,
+                                        const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (launch_empty(launch)) return T4A_OK;
+  if (out == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (axis < 0 || axis >= in_layout->rank || out_layout->rank != in_layout->rank) return T4A_OK;
+  return launch_derived(out, in, dtype, in_layout->rank, in_layout->extents,
+                        t4a::strides_of(nullptr, in_layout->extents), 0,
+                        t4a::strides_of(out_layout->strides, in_layout->extents),
+                        out_layout->offset + axis_offset * out_layout->strides[axis], in_len,
+                        launch, stream);
+}
+
+// The general-rank twins of these entries: the kernels plan in LDS.
+#define T4A_ANY_LAUNCH(kernel, ...)                                                        \
+  do {                                                                                     \
+    if (launch_empty(launch)) return T4A_OK;                                               \
+    const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);                    \
+    const dim3 block(launch->block[0], launch->block[1], launch->block[2]);                \
+    hipLaunchKernelGGL(kernel, grid, block, 0, static_cast<hipStream_t>(stream), __VA_ARGS__); \
+    return status_of_last_launch();                                                        \
+  } while (0)
+
+extern "C" int t4a_hip_fill_zero_view_any(void* out, int dtype,
+                                          const t4a_cuda_layout_any* layout, long long len,
+                                          const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (!launch_empty(launch) && out == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  T4A_ANY_LAUNCH(t4a_cuda_fill_zero_view_any, out, dtype, *layout, len);
+}
+
+extern "C" int t4a_hip_contiguous_to_view_any(void* dst, const void* src, int dtype,
+                                              const t4a_cuda_layout_any* dst_layout,
+                                              long long len, const t4a_launch* launch,
+                                              void* stream) {
+  if (launch == nullptr || dst_layout == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (!launch_empty(launch) && (dst == nullptr || src == nullptr))
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  T4A_ANY_LAUNCH(t4a_cuda_contiguous_to_view_any, dst, src, dtype, *dst_layout, len);
+}
+
+extern "C" int t4a_hip_broadcast_in_dim_any(void* out, const void* in, int dtype,
+                                            const t4a_cuda_layout_any* out_layout,
+                                            const t4a_cuda_layout_any* in_layout,
+                                            const t4a_cuda_axis_values_any* dims,
+                                            long long out_len, const t4a_launch* launch,
+                                            void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr || dims == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (!launch_empty(launch) && (out == nullptr || in == nullptr))
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  T4A_ANY_LAUNCH(t4a_cuda_broadcast_in_dim_any, out, in, dtype, *out_layout, *in_layout, *dims,
+                 out_len);
+}
+
+extern "C" int t4a_hip_concatenate_copy_any(void* out, const void* in, int dtype,
+                                            const t4a_cuda_layout_any* out_layout,
+                                            const t4a_cuda_layout_any* in_layout, int axis,
+                                            long long axis_offset, long long in_len,
+                                            const t4a_launch* launch, void* stream) {
+  if (launch == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (!launch_empty(launch) && (out == nullptr || in == nullptr))
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  T4A_ANY_LAUNCH(t4a_cuda_concatenate_copy_any, out, in, dtype, *out_layout, *in_layout, axis,
+                 axis_offset, in_len);
+}
+
+#undef T4A_ANY_LAUNCH

@@ -124,6 +124,17 @@ int require_destination(const View& l) {
   return ok();
 }
 
+// Reference is_compact (src/lib.rs:424-439).
+bool is_compact(const View& l) {
+  if (l.offset != 0) return false;
+  long long stride = 1;
+  for (int k = 0; k < l.rank; ++k) {
+    if (l.strides[k] != stride) return false;
+    if (!checked_mul(stride, l.extents[k], &stride)) return false;
+  }
+  return true;
+}
+
 bool dtype_known(int dtype) { return t4a::dtype_size(dtype) != 0; }
 
 void set_launch(t4a_launch* out, long long grid, unsigned block, unsigned shared) {
@@ -505,6 +516,121 @@ int plan_reduction(int dtype, int op, const View& out, long long out_len, const 
                      axis, combine_width, &plan->pass2);
 }
 
+// Geometry of a move over derived geometry (contiguous_to_view,
+// broadcast_in_dim, concatenate_copy): the launchers' plan when at most eight
+// fused axes remain, else the general twins' flat walk.
+template <typename SrcStride, typename DstStride>
+void derived_geometry(int rank, const long long* ext, SrcStride src, long long src_offset,
+                      DstStride dst, long long dst_offset, long long len, int es,
+                      t4a_launch* launch) {
+  t4a::MovePlan plan;
+  if (len > 0 && t4a::move_plan_by(&plan, rank, ext, src, src_offset, dst, dst_offset, len, es))
+    movement_launch(plan, es, launch);
+  else
+    set_launch(launch, len == 0 ? 0 : blocks_for(len, kBlock * 4), kBlock, 0);
+}
+
+// Reference plan_fill_zero_view / plan_contiguous_to_view (src/lib.rs:1606-1622,
+// 1641-1658) after the layout checks: the same checks for both.
+int plan_view_entry(int dtype, const View& dst, long long dst_len, long long* len) {
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (int s = element_count(dst, len)) return s;
+  if (int s = require_destination(dst)) return s;
+  if (int s = check_span(dst, dst_len, t4a::dtype_size(dtype))) return s;
+  return flat_launch_check(*len);
+}
+
+int plan_fill_view(int dtype, const View& dst, long long dst_len, t4a_launch* launch) {
+  long long len;
+  if (int s = plan_view_entry(dtype, dst, dst_len, &len)) return s;
+  // A thread per 16-byte vector where the view allows one (the pointer's
+  // alignment is checked at launch; the kernel strides over what is left).
+  const int es = t4a::dtype_size(dtype);
+  const int v = es >= 4 && es <= 8 ? 16 / es : 1;
+  long long fe[t4a::kMaxFusedDims], fs[t4a::kMaxFusedDims], fd[t4a::kMaxFusedDims];
+  const int n = len > 0 ? t4a::fuse_move(dst.rank, dst.extents, dst.strides, dst.strides, fe, fs,
+                                         fd, t4a::kMaxFusedDims)
+                        : 0;
+  t4a::FillPlan fp;
+  const bool vec = t4a::fill_plan(&fp, n, fe, fs, dst.offset, len) && t4a::fill_vectorizable(fp, v);
+  set_launch(launch, len == 0 ? 0 : blocks_for(vec ? len / v : len, kBlock), kBlock, 0);
+  set_variant(launch, dst.rank);
+  return ok();
+}
+
+int plan_contiguous(int dtype, const View& dst, long long dst_len, t4a_launch* launch) {
+  long long len;
+  if (int s = plan_view_entry(dtype, dst, dst_len, &len)) return s;
+  derived_geometry(dst.rank, dst.extents, t4a::strides_of(nullptr, dst.extents), 0,
+                   t4a::strides_of(dst.strides, dst.extents), dst.offset, len,
+                   t4a::dtype_size(dtype), launch);
+  set_variant(launch, dst.rank);
+  return ok();
+}
+
+// Reference plan_broadcast_in_dim (src/lib.rs:1484-1533) after the layout
+// checks; `dims` has `dims_rank` values.
+int plan_broadcast(int dtype, const View& out, long long out_len, const View& in,
+                   long long in_len, const long long* dims, int dims_rank, t4a_launch* launch) {
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (!is_compact(out)) return T4A_ERR_NOT_COMPACT;
+  if (int s = require_destination(out)) return s;
+  if (dims_rank != in.rank) return T4A_ERR_RANK_LENGTH;
+  if (dims_rank > 0 && dims == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  for (int i = 0; i < dims_rank; ++i) {
+    const long long d = dims[i];
+    if (d < 0 || d >= out.rank) return T4A_ERR_INVALID_AXIS;
+    for (int j = 0; j < i; ++j) {
+      if (dims[j] == d) return T4A_ERR_DUPLICATE_AXIS;
+    }
+    const long long ie = in.extents[i];
+    if (ie != out.extents[d] && ie != 1) return T4A_ERR_SHAPE_MISMATCH;
+  }
+  long long len;
+  if (int s = element_count(out, &len)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(in, in_len, es)) return s;
+  if (int s = check_span(out, out_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  derived_geometry(out.rank, out.extents, t4a::BroadcastStrides{dims, dims_rank, in.extents,
+                                                                  in.strides},
+                   in.offset, t4a::strides_of(nullptr, out.extents), 0, len, es, launch);
+  const int widest = out.rank > in.rank ? out.rank : in.rank;
+  set_variant(launch, widest > dims_rank ? widest : dims_rank);
+  return ok();
+}
+
+// Reference plan_concatenate_copy (src/lib.rs:1535-1589) after the layout
+// checks.
+int plan_concatenate(int dtype, const View& out, long long out_len, const View& in,
+                     long long in_len, unsigned axis, long long axis_offset,
+                     t4a_launch* launch) {
+  if (!dtype_known(dtype)) return T4A_ERR_UNSUPPORTED_DTYPE;
+  if (!is_compact(in)) return T4A_ERR_NOT_COMPACT;
+  if (out.rank != in.rank) return T4A_ERR_RANK_LENGTH;
+  if (axis >= static_cast<unsigned>(out.rank)) return T4A_ERR_INVALID_AXIS;
+  if (axis_offset < 0) return T4A_ERR_NEGATIVE_COUNT;
+  if (int s = require_destination(out)) return s;
+  for (int k = 0; k < out.rank; ++k) {
+    if (static_cast<unsigned>(k) != axis && out.extents[k] != in.extents[k])
+      return T4A_ERR_SHAPE_MISMATCH;
+  }
+  long long end;
+  if (!checked_add(axis_offset, in.extents[axis], &end)) return T4A_ERR_OVERFLOW;
+  if (end > out.extents[axis]) return T4A_ERR_SHAPE_MISMATCH;
+  long long len;
+  if (int s = element_count(in, &len)) return s;
+  const int es = t4a::dtype_size(dtype);
+  if (int s = check_span(in, in_len, es)) return s;
+  if (int s = check_span(out, out_len, es)) return s;
+  if (int s = flat_launch_check(len)) return s;
+  derived_geometry(in.rank, in.extents, t4a::strides_of(nullptr, in.extents), 0,
+                   t4a::strides_of(out.strides, in.extents),
+                   out.offset + axis_offset * out.strides[axis], len, es, launch);
+  set_variant(launch, out.rank);
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -808,6 +934,84 @@ int t4a_reduction_partials_layout_any(const t4a_cuda_layout_any* in_layout, unsi
     if (extents[k] < 0) return T4A_ERR_NEGATIVE_EXTENT;
   }
   return ok();
+}
+
+// Reference plan_fill_zero -> plan_elementwise (src/lib.rs:1591-1603): every
+// dtype, flat_launch's refusals; one 16-byte vector per thread.
+int t4a_plan_fill_zero(int dtype, long long len, t4a_launch* launch) {
+  return t4a_plan_copy_exact(dtype, len, launch);
+}
+
+// Reference plan_fill_zero_view (src/lib.rs:1605-1622).
+int t4a_plan_fill_zero_view(int dtype, const t4a_cuda_layout* dst, long long dst_len,
+                            t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(dst)) return s;
+  return plan_fill_view(dtype, V(dst), dst_len, launch);
+}
+
+int t4a_plan_fill_zero_view_any(int dtype, const t4a_cuda_layout_any* dst, long long dst_len,
+                                t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(dst)) return s;
+  return plan_fill_view(dtype, V(dst), dst_len, launch);
+}
+
+// Reference plan_contiguous_to_view (src/lib.rs:1641-1658).
+int t4a_plan_contiguous_to_view(int dtype, const t4a_cuda_layout* dst, long long dst_len,
+                                t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(dst)) return s;
+  return plan_contiguous(dtype, V(dst), dst_len, launch);
+}
+
+int t4a_plan_contiguous_to_view_any(int dtype, const t4a_cuda_layout_any* dst,
+                                    long long dst_len, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(dst)) return s;
+  return plan_contiguous(dtype, V(dst), dst_len, launch);
+}
+
+// Reference plan_broadcast_in_dim (src/lib.rs:1484-1533).
+int t4a_plan_broadcast_in_dim(int dtype, const t4a_cuda_layout* out, long long out_len,
+                              const t4a_cuda_layout* in, long long in_len,
+                              const t4a_cuda_axis_values* dims, t4a_launch* launch) {
+  if (launch == nullptr || dims == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(out)) return s;
+  if (int s = check_layout(in)) return s;
+  if (dims->rank < 0 || dims->rank > T4A_CUDA_MAX_RANK) return T4A_ERR_RANK_LENGTH;
+  return plan_broadcast(dtype, V(out), out_len, V(in), in_len, dims->values, dims->rank,
+                        launch);
+}
+
+int t4a_plan_broadcast_in_dim_any(int dtype, const t4a_cuda_layout_any* out, long long out_len,
+                                  const t4a_cuda_layout_any* in, long long in_len,
+                                  const t4a_cuda_axis_values_any* dims, t4a_launch* launch) {
+  if (launch == nullptr || dims == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(out)) return s;
+  if (int s = check_any(in)) return s;
+  if (dims->rank < 0) return T4A_ERR_RANK_LENGTH;
+  return plan_broadcast(dtype, V(out), out_len, V(in), in_len, dims->values, dims->rank,
+                        launch);
+}
+
+// Reference plan_concatenate_copy (src/lib.rs:1535-1589).
+int t4a_plan_concatenate_copy(int dtype, const t4a_cuda_layout* out, long long out_len,
+                              const t4a_cuda_layout* in, long long in_len, unsigned int axis,
+                              long long axis_offset, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(out)) return s;
+  if (int s = check_layout(in)) return s;
+  return plan_concatenate(dtype, V(out), out_len, V(in), in_len, axis, axis_offset, launch);
+}
+
+int t4a_plan_concatenate_copy_any(int dtype, const t4a_cuda_layout_any* out, long long out_len,
+                                  const t4a_cuda_layout_any* in, long long in_len,
+                                  unsigned int axis, long long axis_offset, t4a_launch* launch) {
+  if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_any(out)) return s;
+  if (int s = check_any(in)) return s;
+  return plan_concatenate(dtype, V(out), out_len, V(in), in_len, axis, axis_offset, launch);
 }
 
 }  // extern "C"

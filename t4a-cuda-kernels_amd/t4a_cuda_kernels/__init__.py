@@ -16,7 +16,8 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import CLaunch, CLayout, CLayoutAny, CReductionPlan, CSplit, CTransposeConfig
+from ._lib import (CAxisValues, CAxisValuesAny, CLaunch, CLayout, CLayoutAny, CReductionPlan,
+                   CSplit, CTransposeConfig)
 
 MAX_RANK = 8
 ABI_REVISION = 14
@@ -456,6 +457,93 @@ def plan_strided_to_strided(dtype: DType, src, src_len: int, dst, dst_len: int) 
                                                        byref(_layout(dst)), dst_len,
                                                        byref(out)))
     return Launch.from_c(out)
+
+
+def plan_fill_zero(dtype: DType, length: int) -> Launch:
+    """Reference plan_fill_zero (src/lib.rs:1601-1603)."""
+    out = CLaunch()
+    _check(_lib.load().t4a_plan_fill_zero(int(dtype), length, byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_fill_zero_view(dtype: DType, dst, dst_len: int) -> Launch:
+    """Reference plan_fill_zero_view (src/lib.rs:1605-1622)."""
+    out = CLaunch()
+    if _wide(dst):
+        _check(_lib.load().t4a_plan_fill_zero_view_any(int(dtype), byref(_any(dst)), dst_len,
+                                                       byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_fill_zero_view(int(dtype), byref(_layout(dst)), dst_len,
+                                                   byref(out)))
+    return Launch.from_c(out)
+
+
+def plan_contiguous_to_view(dtype: DType, dst, dst_len: int) -> Launch:
+    """Reference plan_contiguous_to_view (src/lib.rs:1641-1658)."""
+    out = CLaunch()
+    if _wide(dst):
+        _check(_lib.load().t4a_plan_contiguous_to_view_any(int(dtype), byref(_any(dst)), dst_len,
+                                                           byref(out)))
+    else:
+        _check(_lib.load().t4a_plan_contiguous_to_view(int(dtype), byref(_layout(dst)), dst_len,
+                                                       byref(out)))
+    return Launch.from_c(out)
+
+
+def axis_values(values: Sequence[int]) -> CAxisValues:
+    """t4a_cuda_axis_values over at most eight values (RankLength beyond)."""
+    if len(values) > MAX_RANK:
+        raise T4aError(Error.RankLength + 1)
+    c = CAxisValues()
+    c.rank = len(values)
+    for i, v in enumerate(values):
+        c.values[i] = int(v)
+    return c
+
+
+def axis_values_any(values: Sequence[int], pointer: Optional[int] = None) -> CAxisValuesAny:
+    """t4a_cuda_axis_values_any: over a host copy of `values` (the planners),
+    or over `pointer`, a device copy the caller made (the launchers)."""
+    c = CAxisValuesAny()
+    c.rank = len(values)
+    if pointer is None:
+        arr = (c_longlong * max(len(values), 1))(*values)
+        c.values = ctypes.addressof(arr)
+        c._keep = arr
+    else:
+        c.values = pointer
+    return c
+
+
+def plan_broadcast_in_dim(dtype: DType, out, out_len: int, input, in_len: int,
+                          dims: Sequence[int]) -> Launch:
+    """Reference plan_broadcast_in_dim (src/lib.rs:1484-1533): dims[i] is the
+    destination axis of input axis i."""
+    out_c = CLaunch()
+    if _wide(out, input) or len(dims) > MAX_RANK:
+        _check(_lib.load().t4a_plan_broadcast_in_dim_any(
+            int(dtype), byref(_any(out)), out_len, byref(_any(input)), in_len,
+            byref(axis_values_any(dims)), byref(out_c)))
+    else:
+        _check(_lib.load().t4a_plan_broadcast_in_dim(
+            int(dtype), byref(_layout(out)), out_len, byref(_layout(input)), in_len,
+            byref(axis_values(dims)), byref(out_c)))
+    return Launch.from_c(out_c)
+
+
+def plan_concatenate_copy(dtype: DType, out, out_len: int, input, in_len: int, axis: int,
+                          axis_offset: int) -> Launch:
+    """Reference plan_concatenate_copy (src/lib.rs:1535-1589)."""
+    out_c = CLaunch()
+    if _wide(out, input):
+        _check(_lib.load().t4a_plan_concatenate_copy_any(
+            int(dtype), byref(_any(out)), out_len, byref(_any(input)), in_len, axis, axis_offset,
+            byref(out_c)))
+    else:
+        _check(_lib.load().t4a_plan_concatenate_copy(
+            int(dtype), byref(_layout(out)), out_len, byref(_layout(input)), in_len, axis,
+            axis_offset, byref(out_c)))
+    return Launch.from_c(out_c)
 
 
 def plan_tiled_transpose(dtype: DType, config: TransposeConfig, src_offset: int,

@@ -39,6 +39,19 @@ class CLayoutAny(ctypes.Structure):
     ]
 
 
+class CAxisValues(ctypes.Structure):
+    """t4a_cuda_axis_values: 72 bytes (reference abi.cuh:74-79)."""
+
+    _fields_ = [("rank", c_int), ("reserved", c_int), ("values", c_longlong * MAX_RANK)]
+
+
+class CAxisValuesAny(ctypes.Structure):
+    """t4a_cuda_axis_values_any: 16 bytes, the values by pointer (reference
+    abi.cuh:122-126)."""
+
+    _fields_ = [("rank", c_int), ("reserved", c_int), ("values", c_void_p)]
+
+
 class CTransposeConfig(ctypes.Structure):
     """t4a_cuda_transpose_config: 16 bytes (reference abi.cuh:239-245)."""
 
@@ -80,6 +93,7 @@ assert ctypes.sizeof(CLayout) == 144 and ctypes.alignment(CLayout) == 8
 assert CLayout.offset.offset == 8 and CLayout.extents.offset == 16 and CLayout.strides.offset == 80
 assert ctypes.sizeof(CTransposeConfig) == 16
 assert ctypes.sizeof(CLayoutAny) == 32 and CLayoutAny.extents.offset == 16
+assert ctypes.sizeof(CAxisValues) == 72 and ctypes.sizeof(CAxisValuesAny) == 16
 
 # Every C symbol declared in include/t4a/t4a.h, with its ctypes signature.
 SIGNATURES = {
@@ -158,6 +172,45 @@ SIGNATURES = {
                                             POINTER(CLayoutAny), POINTER(CLayoutAny), c_int,
                                             c_longlong, c_longlong, c_longlong,
                                             POINTER(CLaunch), c_void_p]),
+    "t4a_plan_fill_zero": (c_int, [c_int, c_longlong, POINTER(CLaunch)]),
+    "t4a_plan_fill_zero_view": (c_int, [c_int, POINTER(CLayout), c_longlong, POINTER(CLaunch)]),
+    "t4a_plan_contiguous_to_view": (c_int, [c_int, POINTER(CLayout), c_longlong,
+                                            POINTER(CLaunch)]),
+    "t4a_plan_broadcast_in_dim": (c_int, [c_int, POINTER(CLayout), c_longlong, POINTER(CLayout),
+                                          c_longlong, POINTER(CAxisValues), POINTER(CLaunch)]),
+    "t4a_plan_concatenate_copy": (c_int, [c_int, POINTER(CLayout), c_longlong, POINTER(CLayout),
+                                          c_longlong, c_uint, c_longlong, POINTER(CLaunch)]),
+    "t4a_plan_fill_zero_view_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                            POINTER(CLaunch)]),
+    "t4a_plan_contiguous_to_view_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                                POINTER(CLaunch)]),
+    "t4a_plan_broadcast_in_dim_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                              POINTER(CLayoutAny), c_longlong,
+                                              POINTER(CAxisValuesAny), POINTER(CLaunch)]),
+    "t4a_plan_concatenate_copy_any": (c_int, [c_int, POINTER(CLayoutAny), c_longlong,
+                                              POINTER(CLayoutAny), c_longlong, c_uint,
+                                              c_longlong, POINTER(CLaunch)]),
+    "t4a_hip_fill_zero": (c_int, [c_void_p, c_int, c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_fill_zero_view": (c_int, [c_void_p, c_int, POINTER(CLayout), c_longlong,
+                                       POINTER(CLaunch), c_void_p]),
+    "t4a_hip_contiguous_to_view": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayout),
+                                           c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_broadcast_in_dim": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayout),
+                                         POINTER(CLayout), POINTER(CAxisValues), c_longlong,
+                                         POINTER(CLaunch), c_void_p]),
+    "t4a_hip_concatenate_copy": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayout),
+                                         POINTER(CLayout), c_int, c_longlong, c_longlong,
+                                         POINTER(CLaunch), c_void_p]),
+    "t4a_hip_fill_zero_view_any": (c_int, [c_void_p, c_int, POINTER(CLayoutAny), c_longlong,
+                                           POINTER(CLaunch), c_void_p]),
+    "t4a_hip_contiguous_to_view_any": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayoutAny),
+                                               c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_broadcast_in_dim_any": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayoutAny),
+                                             POINTER(CLayoutAny), POINTER(CAxisValuesAny),
+                                             c_longlong, POINTER(CLaunch), c_void_p]),
+    "t4a_hip_concatenate_copy_any": (c_int, [c_void_p, c_void_p, c_int, POINTER(CLayoutAny),
+                                             POINTER(CLayoutAny), c_int, c_longlong,
+                                             c_longlong, POINTER(CLaunch), c_void_p]),
     "t4a_hip_reduction": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int,
                                   POINTER(CLayout), POINTER(CLayout), c_int, c_longlong,
                                   POINTER(CReductionPlan), c_void_p]),

@@ -65,6 +65,44 @@ def strided_to_strided(dst, src, dtype: DType, src_layout: Layout, dst_layout: L
         byref(launch.to_c()), _stream(stream)))
 
 
+def fill_zero(out, dtype: DType, length: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_fill_zero (cuda/src/movement.cu:514-518)."""
+    _check(_lib.load().t4a_hip_fill_zero(_ptr(out), int(dtype), length, byref(launch.to_c()),
+                                         _stream(stream)))
+
+
+def fill_zero_view(out, dtype: DType, layout: Layout, length: int, launch: Launch,
+                   stream=None) -> None:
+    """Reference t4a_cuda_fill_zero_view (cuda/src/movement.cu:520-526)."""
+    _check(_lib.load().t4a_hip_fill_zero_view(_ptr(out), int(dtype), byref(layout.c), length,
+                                              byref(launch.to_c()), _stream(stream)))
+
+
+def contiguous_to_view(dst, src, dtype: DType, dst_layout: Layout, length: int,
+                       launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_contiguous_to_view (cuda/src/movement.cu:544-551)."""
+    _check(_lib.load().t4a_hip_contiguous_to_view(
+        _ptr(dst), _ptr(src), int(dtype), byref(dst_layout.c), length, byref(launch.to_c()),
+        _stream(stream)))
+
+
+def broadcast_in_dim(out, inp, dtype: DType, out_layout: Layout, in_layout: Layout, dims,
+                     out_len: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_broadcast_in_dim (cuda/src/movement.cu:648-656)."""
+    from . import axis_values
+    _check(_lib.load().t4a_hip_broadcast_in_dim(
+        _ptr(out), _ptr(inp), int(dtype), byref(out_layout.c), byref(in_layout.c),
+        byref(axis_values(dims)), out_len, byref(launch.to_c()), _stream(stream)))
+
+
+def concatenate_copy(out, inp, dtype: DType, out_layout: Layout, in_layout: Layout, axis: int,
+                     axis_offset: int, in_len: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_concatenate_copy (cuda/src/movement.cu:668-676)."""
+    _check(_lib.load().t4a_hip_concatenate_copy(
+        _ptr(out), _ptr(inp), int(dtype), byref(out_layout.c), byref(in_layout.c), axis,
+        axis_offset, in_len, byref(launch.to_c()), _stream(stream)))
+
+
 def reduce(out, inp, dtype: DType, op: ReduceOp, strategy: ReduceStrategy,
            out_layout: Layout, in_layout: Layout, axis: int, output_len: int, launch: Launch,
            stream=None) -> None:
@@ -102,6 +140,38 @@ def strided_to_strided_any(dst, src, dtype: DType, src_layout, dst_layout, lengt
     _check(_lib.load().t4a_hip_strided_to_strided_any(
         _ptr(dst), _ptr(src), int(dtype), byref(src_layout), byref(dst_layout), length,
         byref(launch.to_c()), _stream(stream)))
+
+
+def fill_zero_view_any(out, dtype: DType, layout, length: int, launch: Launch,
+                       stream=None) -> None:
+    """Reference t4a_cuda_fill_zero_view_any (cuda/src/movement.cu:612-618)."""
+    _check(_lib.load().t4a_hip_fill_zero_view_any(_ptr(out), int(dtype), byref(layout), length,
+                                                  byref(launch.to_c()), _stream(stream)))
+
+
+def contiguous_to_view_any(dst, src, dtype: DType, dst_layout, length: int, launch: Launch,
+                           stream=None) -> None:
+    """Reference t4a_cuda_contiguous_to_view_any (cuda/src/movement.cu:629-635)."""
+    _check(_lib.load().t4a_hip_contiguous_to_view_any(
+        _ptr(dst), _ptr(src), int(dtype), byref(dst_layout), length, byref(launch.to_c()),
+        _stream(stream)))
+
+
+def broadcast_in_dim_any(out, inp, dtype: DType, out_layout, in_layout, dims, out_len: int,
+                         launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_broadcast_in_dim_any (cuda/src/movement.cu:658-666); `dims` a
+    t4a_cuda_axis_values_any over device memory."""
+    _check(_lib.load().t4a_hip_broadcast_in_dim_any(
+        _ptr(out), _ptr(inp), int(dtype), byref(out_layout), byref(in_layout), byref(dims),
+        out_len, byref(launch.to_c()), _stream(stream)))
+
+
+def concatenate_copy_any(out, inp, dtype: DType, out_layout, in_layout, axis: int,
+                         axis_offset: int, in_len: int, launch: Launch, stream=None) -> None:
+    """Reference t4a_cuda_concatenate_copy_any (cuda/src/movement.cu:678-685)."""
+    _check(_lib.load().t4a_hip_concatenate_copy_any(
+        _ptr(out), _ptr(inp), int(dtype), byref(out_layout), byref(in_layout), axis,
+        axis_offset, in_len, byref(launch.to_c()), _stream(stream)))
 
 
 def reduce_any(out, inp, dtype: DType, op: ReduceOp, strategy: ReduceStrategy, out_layout,

@@ -16,7 +16,7 @@ HEADER = REPO / "include" / "t4a" / "t4a.h"
 ABI_HEADER = REPO / "include" / "t4a" / "abi.h"
 
 # The reference's kernel entries this library exports under the same names
-# (reference cuda/src/movement.cu:528-646, cuda/src/reduce.cu:765-940), the
+# (reference cuda/src/movement.cu:514-685, cuda/src/reduce.cu:765-940), the
 # general-rank `_any` twins included.
 KERNEL_SYMBOLS = [
     "t4a_cuda_copy_exact",
@@ -29,6 +29,15 @@ KERNEL_SYMBOLS = [
     "t4a_cuda_strided_to_strided_any",
     "t4a_cuda_reduce_any",
     "t4a_cuda_reduce_partials_any",
+    "t4a_cuda_fill_zero",
+    "t4a_cuda_fill_zero_view",
+    "t4a_cuda_fill_zero_view_any",
+    "t4a_cuda_contiguous_to_view",
+    "t4a_cuda_contiguous_to_view_any",
+    "t4a_cuda_broadcast_in_dim",
+    "t4a_cuda_broadcast_in_dim_any",
+    "t4a_cuda_concatenate_copy",
+    "t4a_cuda_concatenate_copy_any",
 ]
 
 
