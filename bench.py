@@ -21,7 +21,9 @@ reference algorithm restated in C, one thread) running whole steps of the same
 workload on the same inputs, repeated for about `--cpu-seconds`.
 
 Other workloads (--workload c1|c1big|c3|c4|c5) run the other BASELINE configs
-the same way; they are for development, the driver's line is c2.
+the same way, `copy` the copy ceiling and `entries` the other movement entries
+(fill_zero, fill_zero_view, contiguous_to_view, broadcast_in_dim,
+concatenate_copy); they are for development, the driver's line is c2.
 """
 from __future__ import annotations
 
@@ -309,7 +311,85 @@ def build_copy() -> Workload:
     return w
 
 
+def build_entries() -> Workload:
+    """The other movement entries at 256 MiB of f32 each: fill_zero, fill_zero_view
+    over every other 32 KiB row, contiguous_to_view into a transposed view,
+    broadcast_in_dim of one row to [8192, 8192], and concatenate_copy of two
+    halves along the inner and the outer axis."""
+    w = Workload("entries", "fill_zero, fill_zero_view, contiguous_to_view, broadcast_in_dim, "
+                 "concatenate_copy over f32 [8192,8192]", "f32")
+    F32 = t.DType.F32
+    n = 8192 * 8192
+    rng = np.random.default_rng(6)
+    host = rng.uniform(-1.0, 1.0, n).astype(np.float32)
+    sets = _sets(host)
+    outs = _empty_like(sets)
+    wide = [hipmem.DeviceBuffer(2 * n * 4) for _ in range(ROTATE)]
+    orc_out = []
+
+    def h_out(nbytes):
+        if not orc_out or orc_out[0].nbytes < nbytes:
+            orc_out[:] = [np.empty(nbytes, dtype=np.uint8)]
+        return orc_out[0]
+
+    plan = t.plan_fill_zero(F32, n)
+    fill = lambda r: hip.fill_zero(outs[r], F32, n, plan, _stream())  # noqa: E731
+    flat = t.Layout.compact([n])
+    w.ops.append(Op("fill_zero_f32", "fill_zero", n * 4, fill, fill, n * 4,
+                    lambda: _oracle().fill_zero_view(h_out(n * 4).view(np.float32), F32, flat,
+                                                     n)))
+
+    rows = t.Layout([8192, 8192], [1, 16384], 0)
+    vplan = t.plan_fill_zero_view(F32, rows, 2 * n)
+    fview = lambda r: hip.fill_zero_view(wide[r], F32, rows, n, vplan, _stream())  # noqa: E731
+    w.ops.append(Op("fill_zero_view_f32_rows", "fill_zero_view", n * 4, fview, fview, n * 4,
+                    lambda: _oracle().fill_zero_view(h_out(2 * n * 4).view(np.float32), F32,
+                                                     rows, n)))
+
+    tr = t.Layout([8192, 8192], [8192, 1], 0)
+    cplan = t.plan_contiguous_to_view(F32, tr, n)
+    scat = lambda r: hip.contiguous_to_view(outs[r], sets[r], F32, tr, n, cplan,  # noqa: E731
+                                            _stream())
+    w.ops.append(Op("contiguous_to_view_f32_transposed", "contiguous_to_view", 2 * n * 4, scat,
+                    scat, 2 * n * 4,
+                    lambda: _oracle().contiguous_to_view(h_out(n * 4).view(np.float32), host,
+                                                         F32, tr, n)))
+
+    out_l = t.Layout.compact([8192, 8192])
+    row = t.Layout.compact([8192])
+    bplan = t.plan_broadcast_in_dim(F32, out_l, n, row, 8192, [0])
+    bc = lambda r: hip.broadcast_in_dim(outs[r], sets[r], F32, out_l, row, [0], n,  # noqa: E731
+                                        bplan, _stream())
+    w.ops.append(Op("broadcast_in_dim_f32_rows", "broadcast_in_dim", (n + 8192) * 4, bc, bc,
+                    (n + 8192) * 4,
+                    lambda: _oracle().broadcast_in_dim(h_out(n * 4).view(np.float32), host, F32,
+                                                       out_l, row, [0], n)))
+
+    for axis, ext, name in ((1, [8192, 4096], "outer"), (0, [4096, 8192], "inner")):
+        half = t.Layout.compact(ext)
+        m = n // 2
+        offs = (0, ext[axis])
+        plans = [t.plan_concatenate_copy(F32, out_l, n, half, m, axis, o) for o in offs]
+
+        def cat(r, half=half, plans=plans, offs=offs, axis=axis, m=m):
+            for o, p in zip(offs, plans):
+                hip.concatenate_copy(outs[r], sets[r], F32, out_l, half, axis, o, m, p,
+                                     _stream())
+
+        def cat_cpu(half=half, offs=offs, axis=axis, m=m):
+            for o in offs:
+                _oracle().concatenate_copy(h_out(n * 4).view(np.float32), host, F32, out_l,
+                                           half, axis, o, m)
+
+        first = lambda r, half=half, p=plans[0], axis=axis, m=m: hip.concatenate_copy(  # noqa: E731
+            outs[r], sets[r], F32, out_l, half, axis, 0, m, p, _stream())
+        w.ops.append(Op(f"concatenate_copy_f32_{name}", "concatenate_copy", 2 * n * 4, cat,
+                        first, 2 * m * 4, cat_cpu))
+    return w
+
+
 WORKLOADS = {
+    "entries": build_entries,
     "copy": build_copy,
     "c2": build_c2,
     "c1": lambda: build_c1(1024),

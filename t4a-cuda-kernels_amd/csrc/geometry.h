@@ -108,6 +108,7 @@ struct FastDiv {
 
 T4A_HD FastDiv fast_div(unsigned int d) {
   FastDiv f;
+  if (d == 0) d = 1;  // no divisor of an empty walk is ever used; keep it defined
   f.d = d;
   int l = 0;
   while ((1ull << l) < d) ++l;
@@ -464,6 +465,57 @@ T4A_HD bool move_plan_by(MovePlan* p, int rank, const long long* ext, SrcStride 
   return true;
 }
 
+// The launchers' form of a CONTIG plan: rows cut into units of V elements (a
+// 16-byte vector when V > 1), one unit per thread of a one-dimensional grid.
+// Unit u is column u % vpr of row u / vpr; the row index is decoded over the
+// other dims, first dim fastest. Every quotient is 32-bit (units < 2^31), so
+// each division is a multiply-high by a precomputed FastDiv.
+struct RowPlan {
+  long long src_offset, dst_offset;
+  unsigned int units;  // rows * vpr
+  unsigned int vpr;    // units per row
+  FastDiv row_div;     // by vpr
+  int n;               // dims other than the row dim
+  FastDiv div[kMaxDims];
+  long long ss[kMaxDims], ds[kMaxDims];
+  bool reread;  // a source stride 0 across rows: the source stays cached
+};
+
+// V = 16 / element size for 1-, 4- and 8-byte elements (1 otherwise) when the
+// rows, offsets and strides keep every unit on V-element boundaries (the
+// launcher also checks the pointers); else 1. False when the plan is not
+// CONTIG or the units reach 2^31.
+T4A_HD bool row_plan(RowPlan* r, const MovePlan& p, int esize, bool vectors) {
+  if (p.mode != kMoveContig || p.row_len <= 0) return false;
+  long long v = vectors && (esize == 1 || esize == 4 || esize == 8) ? 16 / esize : 1;
+  if (v > 1 && (p.row_len % v != 0 || p.src_offset % v != 0 || p.dst_offset % v != 0)) v = 1;
+  for (int k = 0; k < p.n && v > 1; ++k) {
+    if (k != p.row_dim && (p.ss[k] % v != 0 || p.ds[k] % v != 0)) v = 1;
+  }
+  const long long vpr = p.row_len / v;
+  if (p.rows <= 0 || vpr >= (1ll << 31) || p.rows > ((1ll << 31) - 1) / vpr) return false;
+  r->src_offset = p.src_offset;
+  r->dst_offset = p.dst_offset;
+  r->units = static_cast<unsigned int>(p.rows * vpr);
+  r->vpr = static_cast<unsigned int>(vpr);
+  r->row_div = fast_div(r->vpr);
+  r->n = 0;
+  r->reread = false;
+  for (int k = 0; k < p.n; ++k) {
+    if (k == p.row_dim) continue;
+    r->div[r->n] = fast_div(static_cast<unsigned int>(p.ext[k]));
+    r->ss[r->n] = p.ss[k];
+    r->ds[r->n] = p.ds[k];
+    if (p.ss[k] == 0) r->reread = true;
+    ++r->n;
+  }
+  for (int k = r->n; k < kMaxDims; ++k) {
+    r->div[k] = fast_div(1);
+    r->ss[k] = r->ds[k] = 0;
+  }
+  return true;
+}
+
 // fill_zero_view: the view's fused axes (fuse_move with the view's strides on
 // both sides), the stride-1 axis, if any, moved first so that consecutive flat
 // indices are consecutive addresses (every element gets the same zero, so the
@@ -473,19 +525,21 @@ struct FillPlan {
   int n;
   long long ext[kMaxDims];
   long long st[kMaxDims];
+  FastDiv div[kMaxDims];  // by ext[k], when narrow
   long long offset;
   long long len;
-  bool narrow;  // len below 2^32: 32-bit quotients
+  bool narrow;  // len below 2^31: 32-bit quotients by multiply-high
 };
 
 T4A_HD bool fill_plan(FillPlan* p, int n, const long long* fe, const long long* fs,
                       long long offset, long long len) {
   if (n < 0 || n > kMaxDims) return false;
   len = clamp_count(n, fe, len);
+  if (len == 0) n = 0;
   p->n = n;
   p->offset = offset;
   p->len = len;
-  p->narrow = len >= 0 && len < (1ll << 32);
+  p->narrow = len >= 0 && len < (1ll << 31);
   int unit = -1;
   for (int k = 0; k < n; ++k) {
     if (fs[k] == 1 && unit < 0) unit = k;
@@ -506,6 +560,8 @@ T4A_HD bool fill_plan(FillPlan* p, int n, const long long* fe, const long long* 
     p->ext[k] = 1;
     p->st[k] = 0;
   }
+  for (int k = 0; k < kMaxDims; ++k)
+    p->div[k] = fast_div(p->narrow ? static_cast<unsigned int>(p->ext[k]) : 1u);
   return true;
 }
 

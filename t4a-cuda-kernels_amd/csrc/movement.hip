@@ -570,6 +570,43 @@ __device__ __forceinline__ void move_rows(void* dst, const void* src, const Move
   }
 }
 
+// CONTIG rows through a RowPlan (the launchers): one unit of V elements per
+// thread of a kBlock-thread grid of `blocks` <= 2^23 blocks (so the 32-bit
+// unit index and its grid stride stay below 2^32), the row decoded with
+// 32-bit multiply-high quotients; the store streams past the caches, the load
+// too unless the source is read again across rows (a broadcast).
+template <typename P, int V, bool NTL>
+__device__ __forceinline__ void move_row_units(void* dst, const void* src, const RowPlan& rp,
+                                               unsigned int blocks) {
+  P* d = static_cast<P*>(dst);
+  const P* s = static_cast<const P*>(src);
+  const unsigned int gstride = blocks * static_cast<unsigned int>(kBlock);
+  for (unsigned int u = blockIdx.x * static_cast<unsigned int>(kBlock) + threadIdx.x;
+       u < rp.units; u += gstride) {
+    const unsigned int row = div_by(u, rp.row_div);
+    const unsigned int col = u - row * rp.vpr;
+    long long so = rp.src_offset + static_cast<long long>(col) * V;
+    long long dof = rp.dst_offset + static_cast<long long>(col) * V;
+    unsigned int r = row;
+#pragma unroll
+    for (int k = 0; k < kMaxDims; ++k) {
+      if (k >= rp.n) break;
+      const unsigned int q = div_by(r, rp.div[k]);
+      const long long c = static_cast<long long>(r - q * rp.div[k].d);
+      so += c * rp.ss[k];
+      dof += c * rp.ds[k];
+      r = q;
+    }
+    Vec<P, V> x;
+    if constexpr (NTL) {
+      x = nt_load<P, V>(s + so);
+    } else {
+      x = *reinterpret_cast<const Vec<P, V>*>(s + so);
+    }
+    nt_store<P, V>(d + dof, x);
+  }
+}
+
 // GENERIC: one decode per element on both sides.
 template <typename P, int BS>
 __device__ __forceinline__ void move_elements(void* dst, const void* src, const MovePlan& p) {
@@ -779,13 +816,14 @@ __device__ __forceinline__ void fill_body(void* out, long long len, unsigned int
 // fill_zero_view over a FillPlan: V flat indices per thread, stored as one
 // vector when fill_vectorizable (reference movement.cu:78-96 zeroes one element
 // per thread at its decoded address).
-template <typename P, int V>
-__device__ __forceinline__ void fill_view_body(void* out, const FillPlan& fp) {
+template <typename P, int V, int BS>
+__device__ __forceinline__ void fill_view_body(void* out, const FillPlan& fp, unsigned int blocks) {
   P* o = static_cast<P*>(out) + fp.offset;
   const long long units = fp.len / V;
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  const int bs = block_threads<BS>();
+  const long long gstride = static_cast<long long>(blocks) * bs;
   const Vec<P, V> zero{};
-  for (long long u = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; u < units;
+  for (long long u = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; u < units;
        u += gstride) {
     long long off = 0;
     if (fp.narrow) {
@@ -793,9 +831,9 @@ __device__ __forceinline__ void fill_view_body(void* out, const FillPlan& fp) {
 #pragma unroll
       for (int k = 0; k < kMaxDims; ++k) {
         if (k >= fp.n) break;
-        const unsigned int e = static_cast<unsigned int>(fp.ext[k]);
-        off += static_cast<long long>(r % e) * fp.st[k];
-        r /= e;
+        const unsigned int q = div_by(r, fp.div[k]);
+        off += static_cast<long long>(r - q * fp.div[k].d) * fp.st[k];
+        r = q;
       }
     } else {
       long long r = u * V;
@@ -856,9 +894,9 @@ __device__ __forceinline__ void fill_view_entry(void* out, int dtype, int rank, 
       fill_view_wide<P>(out, fused, fe, fs, offset, count);
     } else if (V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                fill_vectorizable(plan, V)) {
-      fill_view_body<P, V>(out, plan);
+      fill_view_body<P, V, 0>(out, plan, gridDim.x);
     } else {
-      fill_view_body<P, 1>(out, plan);
+      fill_view_body<P, 1, 0>(out, plan, gridDim.x);
     }
   };
   switch (es) {
@@ -901,9 +939,16 @@ __global__ void __launch_bounds__(256)
   fill_body<P, BS>(out, len, blocks);
 }
 
-template <typename P, int V>
-__global__ void __launch_bounds__(256) fill_view_kernel(void* out, FillPlan fp) {
-  fill_view_body<P, V>(out, fp);
+template <typename P, int V, int BS>
+__global__ void __launch_bounds__(256)
+    fill_view_kernel(void* out, FillPlan fp, unsigned int blocks) {
+  fill_view_body<P, V, BS>(out, fp, blocks);
+}
+
+template <typename P, int V, bool NTL>
+__global__ void __launch_bounds__(kBlock)
+    move_rows_kernel(void* dst, const void* src, RowPlan rp, unsigned int blocks) {
+  move_row_units<P, V, NTL>(dst, src, rp, blocks);
 }
 
 template <typename P, int VL, int VS, int LA, int LB>
@@ -1167,6 +1212,28 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
   const hipStream_t s = static_cast<hipStream_t>(stream);
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
+    t4a::RowPlan rp;
+    if (plan.mode == t4a::kMoveContig && block.x == static_cast<unsigned>(t4a::kBlock) &&
+        block.y == 1 && block.z == 1 && grid.y == 1 && grid.z == 1 && grid.x <= (1u << 23) &&
+        t4a::row_plan(&rp, plan, static_cast<int>(sizeof(P)),
+                      ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) &
+                       15) == 0)) {
+      constexpr int V = sizeof(P) == 1 ? 16 : sizeof(P) == 4 ? 4 : sizeof(P) == 8 ? 2 : 1;
+      const bool vec = V > 1 && plan.row_len == static_cast<long long>(rp.vpr) * V;
+      if (vec && rp.reread)
+        hipLaunchKernelGGL((t4a::move_rows_kernel<P, V, false>), grid, block, 0, s, dst, src, rp,
+                           grid.x);
+      else if (vec)
+        hipLaunchKernelGGL((t4a::move_rows_kernel<P, V, true>), grid, block, 0, s, dst, src, rp,
+                           grid.x);
+      else if (rp.reread)
+        hipLaunchKernelGGL((t4a::move_rows_kernel<P, 1, false>), grid, block, 0, s, dst, src, rp,
+                           grid.x);
+      else
+        hipLaunchKernelGGL((t4a::move_rows_kernel<P, 1, true>), grid, block, 0, s, dst, src, rp,
+                           grid.x);
+      return status_of_last_launch();
+    }
     if (plan.mode != t4a::kMoveTiled) {
       if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
         hipLaunchKernelGGL((t4a::move_flat_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src,
@@ -1364,10 +1431,19 @@ extern "C" int t4a_hip_fill_zero_view(void* out, int dtype, const t4a_cuda_layou
     using P = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     constexpr int V = t4a::tile_vector<P>();
-    if (V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && t4a::fill_vectorizable(fp, V))
-      hipLaunchKernelGGL((t4a::fill_view_kernel<P, V>), grid, block, 0, s, out, fp);
+    const bool vec =
+        V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && t4a::fill_vectorizable(fp, V);
+    const bool planned = block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock);
+    if (vec && planned)
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, V, t4a::kBlock>), grid, block, 0, s, out, fp,
+                         grid.x);
+    else if (vec)
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, V, 0>), grid, block, 0, s, out, fp, grid.x);
+    else if (planned)
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, 1, t4a::kBlock>), grid, block, 0, s, out, fp,
+                         grid.x);
     else
-      hipLaunchKernelGGL((t4a::fill_view_kernel<P, 1>), grid, block, 0, s, out, fp);
+      hipLaunchKernelGGL((t4a::fill_view_kernel<P, 1, 0>), grid, block, 0, s, out, fp, grid.x);
     return status_of_last_launch();
   });
 }

@@ -175,7 +175,13 @@ void movement_launch(const t4a::MovePlan& plan, int esize, t4a_launch* out) {
       blocks = t4a::tile_plan(&tp, plan, esize) ? plan.tiles
                                                   : (plan.tiles < 1024 ? plan.tiles : 1024);
       break;
-    case t4a::kMoveContig: blocks = blocks_for(plan.len, kBlock * 4); break;
+    // Rows as 16-byte units, one per thread, when the row plan applies.
+    case t4a::kMoveContig: {
+      t4a::RowPlan rp;
+      blocks = t4a::row_plan(&rp, plan, esize, true) ? blocks_for(rp.units, kBlock)
+                                                       : blocks_for(plan.len, kBlock * 4);
+      break;
+    }
     case t4a::kMoveGeneric: blocks = blocks_for(plan.len, kBlock * 4); break;
     default: blocks = 0; break;
   }

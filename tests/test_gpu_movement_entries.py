@@ -315,6 +315,8 @@ BROADCAST_CASES = [
     ([257, 1000], [257], None, 0, [0]),             # column broadcast
     ([64, 3, 128], [128, 64], None, 0, [2, 0]),     # inserted axis and a transpose
     ([7, 5, 3, 2], [3, 1, 7], [1, 0, 3], 2, [2, 3, 0]),
+    ([256, 300], [256], None, 0, [0]),              # whole rows read again: 16-byte units
+    ([64, 5, 48], [64, 48], None, 0, [0, 2]),       # rows decoded over two dims
 ]
 
 
@@ -559,3 +561,37 @@ def test_counts_past_the_layout_stop_at_its_elements():
     d_src = to_device(np.concatenate([src, np.zeros(4096, dtype=np.float32)]))
     hip.contiguous_to_view(d, d_src, F32, lay, n + 4096, plan, stream())
     assert np.array_equal(to_host(d, span * 4), want.view(np.uint8))
+
+
+def test_row_copies_from_unaligned_buffers():
+    """Row copies (a dim contiguous on both sides) through the launchers with
+    both pointers one element past a 16-byte boundary: the element-wise form
+    of the row walk."""
+    rng = np.random.default_rng(72)
+    for dtype in (DType.Bool, F32, F64, DType.C64):
+        es = dtype.size
+        out, inp = Layout.compact([1500, 300]), Layout.compact([1000, 300])
+        n, on = inp.element_count(), out.element_count()
+        src = random_elements(dtype, n + 1, rng)
+        base = random_elements(dtype, on + 1, rng)
+        want = base[1:].copy()
+        orc.concatenate_copy(want, src[1:], dtype, out, inp, 0, 200, n)
+        plan = t.plan_concatenate_copy(dtype, out, on, inp, n, 0, 200)
+        say("concatenate_copy unaligned", dtype.name, plan.grid)
+        d, d_src = to_device(base), to_device(src)
+        hip.concatenate_copy(d.ptr + es, d_src.ptr + es, dtype, out, inp, 0, 200, n, plan,
+                             stream())
+        got = to_host(d, (on + 1) * es)
+        assert np.array_equal(got[:es], base[:1].view(np.uint8)), dtype
+        assert np.array_equal(got[es:], want.view(np.uint8)), dtype
+        # A row broadcast into a shifted destination.
+        o2, row = Layout.compact([256, 40]), Layout.compact([256])
+        want2 = np.zeros(256 * 40, dtype=NUMPY[dtype])
+        orc.broadcast_in_dim(want2, src[1:], dtype, o2, row, [0], 256 * 40)
+        plan = t.plan_broadcast_in_dim(dtype, o2, 256 * 40, row, 256, [0])
+        say("broadcast_in_dim unaligned", dtype.name, plan.grid)
+        d = sentinel((256 * 40 + 1) * es)
+        hip.broadcast_in_dim(d.ptr + es, d_src.ptr + es, dtype, o2, row, [0], 256 * 40, plan,
+                             stream())
+        got = to_host(d, (256 * 40 + 1) * es)
+        assert np.array_equal(got[es:], want2.view(np.uint8)), dtype
