@@ -465,6 +465,31 @@ T4A_HD bool move_plan_by(MovePlan* p, int rank, const long long* ext, SrcStride 
   return true;
 }
 
+// A TILED plan that is one compact 2-D transpose: dim a contiguous in the
+// destination (extent m, source stride n), dim b contiguous in the source
+// (extent n, destination stride m). Then dst[dst_offset + i + j*m] =
+// src[src_offset + i*n + j], the tiled transpose's map with one matrix, and
+// the launchers route it to that kernel's 128 x 128 tiles (16 KiB tiles of the
+// general tiled walk move a square transpose about a tenth slower).
+struct TransposeRoute {
+  long long m, n, src_offset, dst_offset;
+};
+
+T4A_HD bool transpose_route(const MovePlan& p, TransposeRoute* r) {
+  if (p.mode != kMoveTiled || p.n != 2) return false;
+  const int a = p.ds[0] == 1 ? 0 : p.ds[1] == 1 ? 1 : -1;
+  if (a < 0) return false;
+  const int b = 1 - a;
+  if (p.ss[b] != 1 || p.ss[a] != p.ext[b] || p.ds[b] != p.ext[a]) return false;
+  if (p.src_offset < 0 || p.dst_offset < 0) return false;
+  r->m = p.ext[a];
+  r->n = p.ext[b];
+  r->src_offset = p.src_offset;
+  r->dst_offset = p.dst_offset;
+  const TransposeTiling t = transpose_tiling(r->m, r->n, 1, 16);  // the smallest tiles
+  return t.total < (1ll << 30) && r->m < (1ll << 31) && r->n < (1ll << 31);
+}
+
 // The launchers' form of a CONTIG plan: rows cut into units of V elements (a
 // 16-byte vector when V > 1), one unit per thread of a one-dimensional grid.
 // Unit u is column u % vpr of row u / vpr; the row index is decoded over the

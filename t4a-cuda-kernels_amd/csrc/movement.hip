@@ -575,7 +575,7 @@ __device__ __forceinline__ void move_rows(void* dst, const void* src, const Move
 // unit index and its grid stride stay below 2^32), the row decoded with
 // 32-bit multiply-high quotients; the store streams past the caches, the load
 // too unless the source is read again across rows (a broadcast).
-template <typename P, int V, bool NTL>
+template <typename P, int V, bool NTL, int NR>
 __device__ __forceinline__ void move_row_units(void* dst, const void* src, const RowPlan& rp,
                                                unsigned int blocks) {
   P* d = static_cast<P*>(dst);
@@ -589,8 +589,8 @@ __device__ __forceinline__ void move_row_units(void* dst, const void* src, const
     long long dof = rp.dst_offset + static_cast<long long>(col) * V;
     unsigned int r = row;
 #pragma unroll
-    for (int k = 0; k < kMaxDims; ++k) {
-      if (k >= rp.n) break;
+    for (int k = 0; k < (NR >= 0 ? NR : kMaxDims); ++k) {
+      if (NR < 0 && k >= rp.n) break;
       const unsigned int q = div_by(r, rp.div[k]);
       const long long c = static_cast<long long>(r - q * rp.div[k].d);
       so += c * rp.ss[k];
@@ -945,10 +945,12 @@ __global__ void __launch_bounds__(256)
   fill_view_body<P, V, BS>(out, fp, blocks);
 }
 
-template <typename P, int V, bool NTL>
+// NR: the row plan's other-dim count when 0, 1 or 2 (the loop unrolled to
+// exactly those), -1 for any count.
+template <typename P, int V, bool NTL, int NR>
 __global__ void __launch_bounds__(kBlock)
     move_rows_kernel(void* dst, const void* src, RowPlan rp, unsigned int blocks) {
-  move_row_units<P, V, NTL>(dst, src, rp, blocks);
+  move_row_units<P, V, NTL, NR>(dst, src, rp, blocks);
 }
 
 template <typename P, int VL, int VS, int LA, int LB>
@@ -1205,6 +1207,27 @@ void launch_tile_once(bool vl, bool vs, dim3 grid, hipStream_t s, void* dst, con
   launch_tile_shape<P, 1, 1>(grid, s, dst, src, tp);
 }
 
+// A compact 2-D transpose found in a movement plan, on the tiled transpose's
+// kernel: 512-thread blocks, one per tile, in the ordered (diagonal) walk.
+template <typename P>
+int launch_transpose_route(void* dst, const void* src, const t4a::TransposeRoute& r,
+                           hipStream_t s) {
+  constexpr long long TM = t4a::TransposeShape<P>::TM;
+  constexpr long long TN = t4a::TransposeShape<P>::TN;
+  const long long tiles_m = (r.m + TM - 1) / TM;
+  const long long tiles_n = (r.n + TN - 1) / TN;
+  t4a::TileOrder order{};
+  order.tiles_m = t4a::fast_div(static_cast<unsigned int>(tiles_m));
+  order.tiles_n = t4a::fast_div(static_cast<unsigned int>(tiles_n));
+  order.per_batch = static_cast<unsigned int>(tiles_m * tiles_n);
+  order.blocks = order.per_batch;
+  P* d = static_cast<P*>(dst) + r.dst_offset;
+  hipLaunchKernelGGL((t4a::transpose_kernel<P, t4a::kTransposeBlock, true>),
+                     dim3(order.per_batch), dim3(t4a::kTransposeBlock), 0, s, d, src, r.src_offset,
+                     r.m * r.n, r.m, r.n, order);
+  return status_of_last_launch();
+}
+
 int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
                 const t4a_launch* launch, void* stream, int dtype) {
   const dim3 grid(launch->grid[0], launch->grid[1], launch->grid[2]);
@@ -1220,18 +1243,36 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
                        15) == 0)) {
       constexpr int V = sizeof(P) == 1 ? 16 : sizeof(P) == 4 ? 4 : sizeof(P) == 8 ? 2 : 1;
       const bool vec = V > 1 && plan.row_len == static_cast<long long>(rp.vpr) * V;
-      if (vec && rp.reread)
-        hipLaunchKernelGGL((t4a::move_rows_kernel<P, V, false>), grid, block, 0, s, dst, src, rp,
-                           grid.x);
-      else if (vec)
-        hipLaunchKernelGGL((t4a::move_rows_kernel<P, V, true>), grid, block, 0, s, dst, src, rp,
-                           grid.x);
-      else if (rp.reread)
-        hipLaunchKernelGGL((t4a::move_rows_kernel<P, 1, false>), grid, block, 0, s, dst, src, rp,
-                           grid.x);
-      else
-        hipLaunchKernelGGL((t4a::move_rows_kernel<P, 1, true>), grid, block, 0, s, dst, src, rp,
-                           grid.x);
+      auto go = [&](auto v_tag, auto ntl_tag) {
+        constexpr int VV = decltype(v_tag)::value;
+        constexpr bool NTL = decltype(ntl_tag)::value;
+        switch (rp.n) {
+          case 0:
+            hipLaunchKernelGGL((t4a::move_rows_kernel<P, VV, NTL, 0>), grid, block, 0, s, dst,
+                               src, rp, grid.x);
+            break;
+          case 1:
+            hipLaunchKernelGGL((t4a::move_rows_kernel<P, VV, NTL, 1>), grid, block, 0, s, dst,
+                               src, rp, grid.x);
+            break;
+          case 2:
+            hipLaunchKernelGGL((t4a::move_rows_kernel<P, VV, NTL, 2>), grid, block, 0, s, dst,
+                               src, rp, grid.x);
+            break;
+          default:
+            hipLaunchKernelGGL((t4a::move_rows_kernel<P, VV, NTL, -1>), grid, block, 0, s, dst,
+                               src, rp, grid.x);
+            break;
+        }
+      };
+      using Vt = std::integral_constant<int, V>;
+      using V1 = std::integral_constant<int, 1>;
+      using Nt = std::true_type;
+      using Nf = std::false_type;
+      if (vec && rp.reread) go(Vt{}, Nf{});
+      else if (vec) go(Vt{}, Nt{});
+      else if (rp.reread) go(V1{}, Nf{});
+      else go(V1{}, Nt{});
       return status_of_last_launch();
     }
     if (plan.mode != t4a::kMoveTiled) {
@@ -1242,6 +1283,12 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
         hipLaunchKernelGGL((t4a::move_flat_kernel<P, 0>), grid, block, 0, s, dst, src, plan);
       return status_of_last_launch();
     }
+    // A planned tiled geometry whose plan is one compact 2-D transpose takes
+    // the transpose kernel, with that kernel's own grid.
+    t4a::TransposeRoute route;
+    if (block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 && block.z == 1 &&
+        grid.y == 1 && grid.z == 1 && t4a::transpose_route(plan, &route))
+      return launch_transpose_route<P>(dst, src, route, s);
     constexpr int V = t4a::tile_vector<P>();
     bool vl, vs;
     t4a::tile_vectorizable(plan, V, dst, src, &vl, &vs);

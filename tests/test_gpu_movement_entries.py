@@ -595,3 +595,70 @@ def test_row_copies_from_unaligned_buffers():
                              stream())
         got = to_host(d, (256 * 40 + 1) * es)
         assert np.array_equal(got[es:], want2.view(np.uint8)), dtype
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=lambda d: d.name)
+def test_compact_transposes_route_to_the_transpose_kernel(dtype):
+    """A movement whose fused plan is one compact 2-D transpose runs on the
+    tiled transpose's kernel through the launchers: materialize_strided of a
+    transposed view, strided_to_strided and contiguous_to_view into one (with
+    a destination offset), broadcast_in_dim with a swapped map and
+    concatenate_copy into a transposed destination; full and edge tiles,
+    vector and element paths (odd extents, odd offsets)."""
+    rng = np.random.default_rng(73)
+    for m, n, so, do in ((1, 7, 0, 0), (97, 131, 5, 3), (128, 128, 0, 0), (300, 257, 4, 8),
+                         (1024, 768, 0, 4), (64, 2000, 1, 0)):
+        count = m * n
+        src = random_elements(dtype, so + count, rng)
+        d_src = to_device(src)
+        view = Layout([m, n], [n, 1], so)  # the source read as its transpose
+        want = np.zeros(count, dtype=NUMPY[dtype])
+        orc.materialize_strided(want, src, dtype, view, count)
+        plan = t.plan_materialize_strided(dtype, view, so + count)
+        say("route materialize", dtype.name, m, n, so, plan.grid)
+        d = sentinel(count * dtype.size)
+        hip.materialize_strided(d, d_src, dtype, view, count, plan, stream())
+        assert np.array_equal(to_host(d, count * dtype.size), want.view(np.uint8)), (m, n)
+
+        comp = Layout([n, m], [1, n], so)  # compact [n, m] from the offset
+        dst_v = Layout([n, m], [m, 1], do)
+        want = np.frombuffer(bytes([SENTINEL]) * ((do + count) * dtype.size),
+                             dtype=NUMPY[dtype]).copy()
+        orc.strided_to_strided(want, src, dtype, comp, dst_v, count)
+        plan = t.plan_strided_to_strided(dtype, comp, so + count, dst_v, do + count)
+        say("route strided_to_strided", dtype.name, m, n, so, do, plan.grid)
+        d = sentinel((do + count) * dtype.size)
+        hip.strided_to_strided(d, d_src, dtype, comp, dst_v, count, plan, stream())
+        assert np.array_equal(to_host(d, (do + count) * dtype.size), want.view(np.uint8))
+
+        want = np.frombuffer(bytes([SENTINEL]) * ((do + count) * dtype.size),
+                             dtype=NUMPY[dtype]).copy()
+        orc.contiguous_to_view(want, src, dtype, dst_v, count)
+        plan = t.plan_contiguous_to_view(dtype, dst_v, do + count)
+        say("route contiguous_to_view", dtype.name, m, n, do, plan.grid)
+        d = sentinel((do + count) * dtype.size)
+        hip.contiguous_to_view(d, d_src, dtype, dst_v, count, plan, stream())
+        assert np.array_equal(to_host(d, (do + count) * dtype.size), want.view(np.uint8))
+
+        out, inp = Layout.compact([m, n]), Layout.compact([n, m])
+        want = np.zeros(count, dtype=NUMPY[dtype])
+        orc.broadcast_in_dim(want, src, dtype, out, inp, [1, 0], count)
+        plan = t.plan_broadcast_in_dim(dtype, out, count, inp, count + so, [1, 0])
+        say("route broadcast_in_dim", dtype.name, m, n, plan.grid)
+        d = sentinel(count * dtype.size)
+        hip.broadcast_in_dim(d, d_src, dtype, out, inp, [1, 0], count, plan, stream())
+        assert np.array_equal(to_host(d, count * dtype.size), want.view(np.uint8))
+
+        # concatenate into columns [2, 2 + n) of a [m, n + 3] destination seen
+        # transposed: out extents [n + 3, m] strides [m, 1]
+        o2 = Layout([n + 3, m], [m, 1], 0)
+        i2 = Layout.compact([n, m])
+        span = (n + 3) * m
+        base = random_elements(dtype, span, rng)
+        want = base.copy()
+        orc.concatenate_copy(want, src, dtype, o2, i2, 0, 2, count)
+        plan = t.plan_concatenate_copy(dtype, o2, span, i2, count, 0, 2)
+        say("route concatenate_copy", dtype.name, m, n, plan.grid)
+        d = to_device(base)
+        hip.concatenate_copy(d, d_src, dtype, o2, i2, 0, 2, count, plan, stream())
+        assert np.array_equal(to_host(d, span * dtype.size), want.view(np.uint8))
