@@ -1551,7 +1551,9 @@ extern "C" int t4a_hip_concatenate_copy(void* out, const void* in, int dtype,
     return T4A_HIP_ERR_NULL_ARGUMENT;
   if (launch_empty(launch)) return T4A_OK;
   if (out == nullptr || in == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
-  if (axis < 0 || axis >= in_layout->rank || out_layout->rank != in_layout->rank) return T4A_OK;
+  if (in_layout->rank > t4a::kMaxDims || axis < 0 || axis >= in_layout->rank ||
+      out_layout->rank != in_layout->rank)
+    return T4A_OK;
   return launch_derived(out, in, dtype, in_layout->rank, in_layout->extents,
                         t4a::strides_of(nullptr, in_layout->extents), 0,
                         t4a::strides_of(out_layout->strides, in_layout->extents),
