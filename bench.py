@@ -63,6 +63,12 @@ TRAFFIC: dict[tuple[str, str], dict] = {
     ("c4", "sumsq_f32_middle"): {"bytes": 539009101, "source": "profiles/traffic_c4_sumsq_f32_middle.md"},
     ("c4", "prod_i32_last"): {"bytes": 671012891, "source": "profiles/traffic_c4_prod_i32_last.md"},
     ("c5", "permute6_c64"): {"bytes": 537005613, "source": "profiles/traffic_c5_permute6_c64.md"},
+    ("entries", "contiguous_to_view_f32_transposed"): {"bytes": 536883971, "source": "profiles/traffic_entries_contiguous_to_view_f32_transposed.md"},
+    ("entries", "broadcast_in_dim_f32_rows"): {"bytes": 268405994, "source": "profiles/traffic_entries_broadcast_in_dim_f32_rows.md"},
+    ("entries", "concatenate_copy_f32_inner"): {"bytes": 268421058, "source": "profiles/traffic_entries_concatenate_copy_f32_inner.md"},
+    ("entries", "concatenate_copy_f32_outer"): {"bytes": 268472325, "source": "profiles/traffic_entries_concatenate_copy_f32_outer.md"},
+    ("entries", "fill_zero_f32"): {"bytes": 268378148, "source": "profiles/traffic_entries_fill_zero_f32.md"},
+    ("entries", "fill_zero_view_f32_rows"): {"bytes": 268247785, "source": "profiles/traffic_entries_fill_zero_view_f32_rows.md"},
 }
 
 NUMPY_DTYPE = {t.DType.F32: np.float32, t.DType.F64: np.float64, t.DType.I32: np.int32,
