@@ -490,6 +490,10 @@ T4A_HD bool transpose_route(const MovePlan& p, TransposeRoute* r) {
   return t.total < (1ll << 30) && r->m < (1ll << 31) && r->n < (1ll << 31);
 }
 
+// A CONTIG plan of one fused dim: one run contiguous on both sides from the
+// two offsets, which the launchers move as copy_exact moves a buffer.
+T4A_HD bool linear_route(const MovePlan& p) { return p.mode == kMoveContig && p.n == 1; }
+
 // The launchers' form of a CONTIG plan: rows cut into units of V elements (a
 // 16-byte vector when V > 1), one unit per thread of a one-dimensional grid.
 // Unit u is column u % vpr of row u / vpr; the row index is decoded over the

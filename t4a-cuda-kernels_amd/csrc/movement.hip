@@ -1235,6 +1235,14 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
   const hipStream_t s = static_cast<hipStream_t>(stream);
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
+    const bool flat_grid = block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 &&
+                           block.z == 1 && grid.y == 1 && grid.z == 1;
+    if (flat_grid && t4a::linear_route(plan)) {
+      hipLaunchKernelGGL((t4a::copy_kernel<P, t4a::kBlock>), grid, block, 0, s,
+                         static_cast<P*>(dst) + plan.dst_offset,
+                         static_cast<const P*>(src) + plan.src_offset, plan.len, grid.x);
+      return status_of_last_launch();
+    }
     t4a::RowPlan rp;
     if (plan.mode == t4a::kMoveContig && block.x == static_cast<unsigned>(t4a::kBlock) &&
         block.y == 1 && block.z == 1 && grid.y == 1 && grid.z == 1 && grid.x <= (1u << 23) &&

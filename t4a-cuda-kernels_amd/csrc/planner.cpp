@@ -175,11 +175,15 @@ void movement_launch(const t4a::MovePlan& plan, int esize, t4a_launch* out) {
       blocks = t4a::tile_plan(&tp, plan, esize) ? plan.tiles
                                                   : (plan.tiles < 1024 ? plan.tiles : 1024);
       break;
-    // Rows as 16-byte units, one per thread, when the row plan applies.
+    // One run: copy_exact's geometry (a 16-byte vector per thread). Rows as
+    // 16-byte units, one per thread, when the row plan applies.
     case t4a::kMoveContig: {
       t4a::RowPlan rp;
-      blocks = t4a::row_plan(&rp, plan, esize, true) ? blocks_for(rp.units, kBlock)
-                                                       : blocks_for(plan.len, kBlock * 4);
+      if (t4a::linear_route(plan))
+        blocks = blocks_for(plan.len * esize, kBlock * 16);
+      else
+        blocks = t4a::row_plan(&rp, plan, esize, true) ? blocks_for(rp.units, kBlock)
+                                                         : blocks_for(plan.len, kBlock * 4);
       break;
     }
     case t4a::kMoveGeneric: blocks = blocks_for(plan.len, kBlock * 4); break;
