@@ -2,7 +2,7 @@
 single-axis reduction path on one MI355X.
 
 `python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]` prints ONE
-JSON line. The default workload is BASELINE.json's configs[1] (C2): f32
+JSON line. The default workload is benchmark configuration C2: f32
 [8192, 8192] sum and max over the inner (contiguous) and the outer axis, and an
 i64 sum over the inner axis, each a planned reduction (pass 1 + combine)
 launched through the C ABI. One step = those five reductions over one input
@@ -20,7 +20,7 @@ known size, recorded in TRAFFIC below. `cpu_baseline` is the CPU oracle (the
 reference algorithm restated in C, one thread) running whole steps of the same
 workload on the same inputs, repeated for about `--cpu-seconds`.
 
-Other workloads (--workload c1|c1big|c3|c4|c5) run the other BASELINE configs
+Other workloads (--workload c1|c1big|c3|c4|c5) run the other benchmark configs
 the same way, `copy` the copy ceiling and `entries` the other movement entries
 (fill_zero, fill_zero_view, contiguous_to_view, broadcast_in_dim,
 concatenate_copy); they are for development, the driver's line is c2.

@@ -302,7 +302,7 @@ def test_reduction_partials_layout_is_compact_with_the_split_axis():
 
 
 def test_configuration_plans():
-    """The plans of the BASELINE configurations (reference axis order)."""
+    """The plans of the benchmark configurations C1-C5 (reference axis order)."""
     inp = Layout.compact([8192, 8192])
     plan = t.plan_reduction(DType.F32, ReduceOp.Sum, Layout.compact([1, 8192]), 8192, inp,
                             8192 * 8192, 0, 32)
