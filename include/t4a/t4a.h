@@ -129,6 +129,29 @@ int t4a_plan_materialize_strided(int dtype, const t4a_cuda_layout* src, long lon
 int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long src_len,
                                 const t4a_cuda_layout* dst, long long dst_len,
                                 t4a_launch* launch);
+/* The kernel the t4a_hip_* movement launchers run for a source/destination
+ * pair under its planned geometry (no reference counterpart: the reference
+ * leaves route selection to its consumer, which fuses axes and then picks the
+ * tiled transpose or a strided copy). materialize_strided is the pair with
+ * `dst` NULL (the compact destination); contiguous_to_view, broadcast_in_dim
+ * and concatenate_copy are moves over the pairs their geometry implies.
+ * Alignment only decides between 16-byte and element accesses inside a route. */
+typedef enum {
+  T4A_MOVE_ROUTE_EMPTY = 0,     /* nothing to move */
+  T4A_MOVE_ROUTE_LINEAR = 1,    /* one run contiguous on both sides: the copy kernel */
+  T4A_MOVE_ROUTE_ROWS = 2,      /* a dim contiguous on both sides: 16-byte row units */
+  T4A_MOVE_ROUTE_TRANSPOSE = 3, /* one compact 2-D transpose: the tiled transpose's kernel */
+  T4A_MOVE_ROUTE_TILE_ONCE = 4, /* one 16 KiB LDS tile per block */
+  T4A_MOVE_ROUTE_TILES = 5,     /* persistent blocks walking LDS tiles */
+  T4A_MOVE_ROUTE_ELEMENTS = 6   /* one decode per element */
+} t4a_move_route;
+
+/* Validates as t4a_plan_strided_to_strided (or t4a_plan_materialize_strided
+ * when dst is NULL) with spans of exactly the layouts' reach, then writes the
+ * route to *route. */
+int t4a_plan_move_route(int dtype, const t4a_cuda_layout* src, const t4a_cuda_layout* dst,
+                        int* route);
+
 /* Reference plan_fill_zero (src/lib.rs:1601-1603). */
 int t4a_plan_fill_zero(int dtype, long long len, t4a_launch* launch);
 /* Reference plan_fill_zero_view (src/lib.rs:1605-1622). */

@@ -297,6 +297,41 @@ void movement_geometry(const View& src, const long long* dst_strides, long long 
   set_variant(launch, src.rank);
 }
 
+// The launchers' route for a planned move (their choices in launch_move, in
+// the same order, under the planner's own geometry).
+int move_route(const View& src, const long long* dst_strides, long long dst_offset,
+               long long len, int es) {
+  if (len <= 0) return T4A_MOVE_ROUTE_EMPTY;
+  long long fe[t4a::kMaxFusedDims], fs[t4a::kMaxFusedDims], fd[t4a::kMaxFusedDims];
+  const int n =
+      t4a::fuse_move(src.rank, src.extents, src.strides, dst_strides, fe, fs, fd,
+                     t4a::kMaxFusedDims);
+  if (n < 0 || n > t4a::kMaxDims) return T4A_MOVE_ROUTE_ELEMENTS;
+  t4a::MovePlan plan;
+  t4a::move_plan_view(&plan, n, src.offset, fe, fs, fd, dst_offset, len, es);
+  t4a_launch launch;
+  movement_launch(plan, es, &launch);
+  t4a::RowPlan rp;
+  t4a::TransposeRoute tr;
+  t4a::TilePlan tp;
+  switch (plan.mode) {
+    case t4a::kMoveEmpty: return T4A_MOVE_ROUTE_EMPTY;
+    case t4a::kMoveGeneric: return T4A_MOVE_ROUTE_ELEMENTS;
+    case t4a::kMoveContig:
+      if (t4a::linear_route(plan)) return T4A_MOVE_ROUTE_LINEAR;
+      return t4a::row_plan(&rp, plan, es, true) && launch.grid[0] <= (1u << 23)
+                 ? T4A_MOVE_ROUTE_ROWS
+                 : T4A_MOVE_ROUTE_ELEMENTS;
+    case t4a::kMoveTiled:
+      if (t4a::transpose_route(plan, &tr)) return T4A_MOVE_ROUTE_TRANSPOSE;
+      if (es >= 4 && static_cast<long long>(launch.grid[0]) == plan.tiles &&
+          t4a::tile_plan(&tp, plan, es))
+        return T4A_MOVE_ROUTE_TILE_ONCE;
+      return T4A_MOVE_ROUTE_TILES;
+    default: return T4A_MOVE_ROUTE_ELEMENTS;
+  }
+}
+
 // Reference plan_materialize_strided (src/lib.rs:1628-1641) after the layout
 // checks.
 int plan_materialize(int dtype, const View& src, long long src_len, t4a_launch* launch) {
@@ -739,6 +774,33 @@ int t4a_plan_strided_to_strided(int dtype, const t4a_cuda_layout* src, long long
   if (int s = check_layout(src)) return s;
   if (int s = check_layout(dst)) return s;
   return plan_strided(dtype, V(src), src_len, V(dst), dst_len, launch);
+}
+
+int t4a_plan_move_route(int dtype, const t4a_cuda_layout* src, const t4a_cuda_layout* dst,
+                        int* route) {
+  if (route == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (int s = check_layout(src)) return s;
+  if (dst != nullptr) {
+    if (int s = check_layout(dst)) return s;
+  }
+  const View sv = V(src);
+  long long src_reach;
+  if (int s = reachable_offset(sv, true, &src_reach)) return s;
+  t4a_launch launch;
+  long long len;
+  if (dst == nullptr) {
+    if (int s = plan_materialize(dtype, sv, src_reach + 1, &launch)) return s;
+    if (int s = element_count(sv, &len)) return s;
+    *route = move_route(sv, nullptr, 0, len, t4a::dtype_size(dtype));
+    return ok();
+  }
+  const View dv = V(dst);
+  long long dst_reach;
+  if (int s = reachable_offset(dv, true, &dst_reach)) return s;
+  if (int s = plan_strided(dtype, sv, src_reach + 1, dv, dst_reach + 1, &launch)) return s;
+  if (int s = element_count(sv, &len)) return s;
+  *route = move_route(sv, dv.strides, dv.offset, len, t4a::dtype_size(dtype));
+  return ok();
 }
 
 int t4a_plan_strided_to_strided_any(int dtype, const t4a_cuda_layout_any* src,

@@ -353,6 +353,18 @@ class RankVariant(enum.IntEnum):
     General = 1
 
 
+class MoveRoute(enum.IntEnum):
+    """The kernel the movement launchers run for a layout pair (t4a_move_route)."""
+
+    Empty = 0
+    Linear = 1     # one run contiguous on both sides: the copy kernel
+    Rows = 2       # a dim contiguous on both sides: 16-byte row units
+    Transpose = 3  # one compact 2-D transpose: the tiled transpose's kernel
+    TileOnce = 4   # one 16 KiB LDS tile per block
+    Tiles = 5      # persistent blocks walking LDS tiles
+    Elements = 6   # one decode per element
+
+
 @dataclass(frozen=True)
 class Launch:
     """Planned geometry (reference src/lib.rs:840-873)."""
@@ -457,6 +469,18 @@ def plan_strided_to_strided(dtype: DType, src, src_len: int, dst, dst_len: int) 
                                                        byref(_layout(dst)), dst_len,
                                                        byref(out)))
     return Launch.from_c(out)
+
+
+def move_route(dtype: DType, src: Layout, dst: Optional[Layout] = None) -> MoveRoute:
+    """The route of strided_to_strided(src -> dst), or of materialize_strided
+    when `dst` is None, validated as those planners validate (spans of exactly
+    the layouts' reach). No reference counterpart: route selection is the
+    consumer's there."""
+    out = c_int()
+    _check(_lib.load().t4a_plan_move_route(int(dtype), byref(_layout(src)),
+                                           byref(_layout(dst)) if dst is not None else None,
+                                           byref(out)))
+    return MoveRoute(out.value)
 
 
 def plan_fill_zero(dtype: DType, length: int) -> Launch:
@@ -645,4 +669,7 @@ __all__ = [
     "T4aError", "TransposeConfig", "abi_revision", "plan_copy_exact", "plan_materialize_strided",
     "plan_reduce", "plan_reduce_partials", "plan_reduction", "plan_strided_to_strided",
     "plan_tiled_transpose", "reduction_partials_layout", "split_policy",
+    "MoveRoute", "WideLayout", "axis_values", "axis_values_any", "move_route",
+    "plan_broadcast_in_dim", "plan_concatenate_copy", "plan_contiguous_to_view",
+    "plan_fill_zero", "plan_fill_zero_view",
 ]

@@ -109,6 +109,8 @@ SIGNATURES = {
                                              POINTER(CLaunch)]),
     "t4a_plan_strided_to_strided": (c_int, [c_int, POINTER(CLayout), c_longlong,
                                             POINTER(CLayout), c_longlong, POINTER(CLaunch)]),
+    "t4a_plan_move_route": (c_int, [c_int, POINTER(CLayout), POINTER(CLayout),
+                                    POINTER(c_int)]),
     "t4a_transpose_config_new": (c_int, [c_int, c_int, c_int, c_int,
                                          POINTER(CTransposeConfig)]),
     "t4a_transpose_config_default": (CTransposeConfig, []),
