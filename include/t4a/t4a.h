@@ -64,8 +64,10 @@ typedef enum {
   T4A_ERR_UNSUPPORTED_OP = 25,
   /* Launch-side statuses of the t4a_hip_* functions (no reference counterpart:
    * the reference returns nothing from a raw launch). */
-  T4A_HIP_ERR_LAUNCH = 100,       /* the HIP runtime refused the launch */
-  T4A_HIP_ERR_NULL_ARGUMENT = 101 /* a required pointer argument is NULL */
+  T4A_HIP_ERR_LAUNCH = 100,        /* the HIP runtime refused the launch */
+  T4A_HIP_ERR_NULL_ARGUMENT = 101, /* a required pointer argument is NULL */
+  T4A_HIP_ERR_NOT_FOUND = 102,     /* no such code object, or the library's path is unknown */
+  T4A_HIP_ERR_TOO_SMALL = 103      /* a caller's buffer cannot hold the result */
 } t4a_status;
 
 /* Reference RankVariant (src/lib.rs:800-838): FAST selects the by-value symbol. */
@@ -355,6 +357,29 @@ int t4a_hip_reduction_joins(const void* in, int dtype, int op, const t4a_cuda_la
 /* The hipError_t of the most recent launch on this thread that returned
  * T4A_HIP_ERR_LAUNCH (0 if none). */
 int t4a_hip_last_error(void);
+
+/* ---- code objects (the prepare step's artifacts) -------------------------- */
+
+/* The gfx950 code objects exporting the reference-named kernel entries, built
+ * ahead of time next to libt4a_hip.so. The reference hands its CUDA text to the
+ * consumer's NVRTC (src/lib.rs:32-130, `source::MODULES` / `module_of`) inside a
+ * prepare step that loads modules privately per runtime
+ * (docs/design/cubecl-kernel-port.md:88-109); here prepare is loading these
+ * files (hipModuleLoadData) and binding entries by name (hipModuleGetFunction).
+ * Names and files are static strings; nothing here loads or allocates. */
+int t4a_code_object_count(void);
+const char* t4a_code_object_name(int index);     /* "movement", "reduce"; NULL past the end */
+const char* t4a_code_object_file(int index);     /* "t4a_movement.gfx950.hsaco", ... */
+const char* t4a_code_object_target(void);        /* "gfx950" */
+int t4a_code_object_entry_count(int index);
+const char* t4a_code_object_entry(int index, int entry);
+/* Index of the code object exporting `entry`, -1 for an entry none exports
+ * (reference source::module_of). */
+int t4a_code_object_of(const char* entry);
+/* The code object's absolute path (the library's directory + its file) into
+ * `path` of `capacity` bytes: T4A_HIP_ERR_NOT_FOUND for a bad index,
+ * T4A_HIP_ERR_TOO_SMALL when it does not fit. */
+int t4a_code_object_path(int index, char* path, unsigned long capacity);
 
 #ifdef __cplusplus
 }  /* extern "C" */

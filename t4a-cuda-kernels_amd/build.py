@@ -33,7 +33,7 @@ LIB_NAME = "libt4a_hip.so"
 ARCH = "gfx950"
 
 HIP_SOURCES = ["movement.hip", "reduce.hip"]
-CXX_SOURCES = ["planner.cpp"]
+CXX_SOURCES = ["planner.cpp", "code_objects.cpp"]
 
 
 def code_object_name(source: str) -> str:

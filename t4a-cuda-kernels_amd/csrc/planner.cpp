@@ -699,6 +699,8 @@ const char* t4a_status_name(int status) {
     return names[status];
   if (status == T4A_HIP_ERR_LAUNCH) return "HipLaunch";
   if (status == T4A_HIP_ERR_NULL_ARGUMENT) return "NullArgument";
+  if (status == T4A_HIP_ERR_NOT_FOUND) return "NotFound";
+  if (status == T4A_HIP_ERR_TOO_SMALL) return "TooSmall";
   return "Unknown";
 }
 

@@ -99,6 +99,14 @@ assert ctypes.sizeof(CAxisValues) == 72 and ctypes.sizeof(CAxisValuesAny) == 16
 SIGNATURES = {
     "t4a_abi_revision": (c_int, []),
     "t4a_status_name": (c_char_p, [c_int]),
+    "t4a_code_object_count": (c_int, []),
+    "t4a_code_object_name": (c_char_p, [c_int]),
+    "t4a_code_object_file": (c_char_p, [c_int]),
+    "t4a_code_object_target": (c_char_p, []),
+    "t4a_code_object_entry_count": (c_int, [c_int]),
+    "t4a_code_object_entry": (c_char_p, [c_int, c_int]),
+    "t4a_code_object_of": (c_int, [c_char_p]),
+    "t4a_code_object_path": (c_int, [c_int, c_char_p, ctypes.c_ulong]),
     "t4a_dtype_size": (c_int, [c_int]),
     "t4a_layout_new": (c_int, [POINTER(CLayout), c_int, POINTER(c_longlong),
                                POINTER(c_longlong), c_longlong]),
