@@ -380,7 +380,8 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
 // separates the loads) and are neither parked nor stored.
 template <typename P, int VL, int VS, int LA, int LB>
 __device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __restrict__ src,
-                                               const TilePlan& tp, P* tile) {
+                                               const TilePlan& tp, P* tile,
+                                               unsigned int tile_index) {
   constexpr int BS = kBlock;
   constexpr int PITCH = LB + 1;
   constexpr int LBV = LB / VL;
@@ -388,7 +389,7 @@ __device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __r
   constexpr int RL = LA * LBV / BS;
   constexpr int RS = LB * LAV / BS;
   static_assert(RL * BS == LA * LBV && RS * BS == LB * LAV, "the block divides the tile");
-  unsigned int rest = blockIdx.x;
+  unsigned int rest = tile_index;
   unsigned int first = 0, ta = 0, tb = 0;
   long long sb = tp.src_offset;
   long long db = tp.dst_offset;
@@ -629,12 +630,112 @@ __device__ __forceinline__ void move_elements(void* dst, const void* src, const 
   }
 }
 
+// A value every lane holds alike, read out of LDS into scalar registers (one
+// readfirstlane per dword), so that a loop reads it without LDS traffic.
+template <typename T>
+__device__ __forceinline__ T uniform_copy(const T& shared_value) {
+  static_assert(sizeof(T) % 4 == 0, "whole dwords");
+  unsigned int words[sizeof(T) / 4];
+  __builtin_memcpy(words, &shared_value, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(T) / 4); ++i)
+    words[i] = __builtin_amdgcn_readfirstlane(words[i]);
+  T out;
+  __builtin_memcpy(&out, words, sizeof(T));
+  return out;
+}
+
+// TILED inside the entries: when the plan has a one-tile shape (tile_plan),
+// thread 0 writes the TilePlan into the block's move scratch behind the tile,
+// and the block moves tiles blockIdx.x, blockIdx.x + gridDim.x, ... with the
+// launchers' one-tile body, so a persistent grid plans once per block; other
+// plans and block sizes take the pipelined tile walk.
+template <typename P>
+__device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, const MovePlan& p,
+                                                 unsigned char* lds) {
+  if constexpr (sizeof(P) >= 4) {
+    constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
+    constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
+    constexpr int kTileBytes = LA * (LB + 1) * static_cast<int>(sizeof(P));
+    static_assert(kTileBytes + static_cast<int>(sizeof(TilePlan)) <= kMoveLdsBytes,
+                  "the tile and its plan share the move scratch");
+    if (blockDim.x == static_cast<unsigned>(kBlock)) {
+      TilePlan* shared_tp = reinterpret_cast<TilePlan*>(lds + kTileBytes);
+      __shared__ int once_ok;
+      if (threadIdx.x == 0) once_ok = tile_plan(shared_tp, p, static_cast<int>(sizeof(P))) ? 1 : 0;
+      __syncthreads();
+      if (once_ok) {
+        constexpr int V = tile_vector<P>();
+        bool vl, vs;
+        tile_vectorizable(p, V, dst, src, &vl, &vs);
+        P* tile = reinterpret_cast<P*>(lds);
+        const unsigned int tiles = static_cast<unsigned int>(p.tiles);
+        const TilePlan tp = uniform_copy(*shared_tp);
+        auto walk = [&](auto vl_tag, auto vs_tag) {
+          constexpr int VLt = decltype(vl_tag)::value;
+          constexpr int VSt = decltype(vs_tag)::value;
+          for (unsigned int t = blockIdx.x; t < tiles; t += gridDim.x) {
+            move_tile_once<P, VLt, VSt, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src),
+                                                tp, tile, t);
+            __syncthreads();  // the tile's LDS is rewritten by the next one
+          }
+        };
+        using VV = std::integral_constant<int, V>;
+        using V1 = std::integral_constant<int, 1>;
+        if (vl && vs) walk(VV{}, VV{});
+        else if (vl) walk(VV{}, V1{});
+        else if (vs) walk(V1{}, VV{});
+        else walk(V1{}, V1{});
+        return;
+      }
+    }
+  }
+  move_tiled<P>(dst, src, p, lds);
+}
+
+
+// CONTIG inside the entries: thread 0 turns the LDS plan into the launchers'
+// RowPlan (in the block's move scratch, unused by rows), every lane copies it
+// to scalar registers and walks 16-byte row units as the launchers do. Other
+// block sizes, and plans the row walk cannot take, decode per element.
+template <typename P>
+__device__ __forceinline__ void move_rows_entry(void* dst, const void* src, const MovePlan& p,
+                                                unsigned char* lds) {
+  if (blockDim.x != static_cast<unsigned>(kBlock) || gridDim.x > (1u << 23)) {
+    move_rows<P, 0>(dst, src, p);
+    return;
+  }
+  RowPlan* shared_rp = reinterpret_cast<RowPlan*>(lds);
+  __shared__ int rows_ok;
+  if (threadIdx.x == 0) {
+    const bool aligned =
+        ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    rows_ok = row_plan(shared_rp, p, static_cast<int>(sizeof(P)), aligned) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!rows_ok) {
+    move_rows<P, 0>(dst, src, p);
+    return;
+  }
+  const RowPlan rp = uniform_copy(*shared_rp);
+  constexpr int V = sizeof(P) == 1 ? 16 : sizeof(P) == 4 ? 4 : sizeof(P) == 8 ? 2 : 1;
+  const bool vec = V > 1 && p.row_len == static_cast<long long>(rp.vpr) * V;
+  if (vec && rp.reread)
+    move_row_units<P, V, false, -1>(dst, src, rp, gridDim.x);
+  else if (vec)
+    move_row_units<P, V, true, -1>(dst, src, rp, gridDim.x);
+  else if (rp.reread)
+    move_row_units<P, 1, false, -1>(dst, src, rp, gridDim.x);
+  else
+    move_row_units<P, 1, true, -1>(dst, src, rp, gridDim.x);
+}
+
 template <typename P>
 __device__ __forceinline__ void move_dispatch(void* dst, const void* src, const MovePlan& p,
                                               unsigned char* lds) {
   switch (p.mode) {
-    case kMoveTiled: move_tiled<P>(dst, src, p, lds); break;
-    case kMoveContig: move_rows<P, 0>(dst, src, p); break;
+    case kMoveTiled: move_tiled_entry<P>(dst, src, p, lds); break;
+    case kMoveContig: move_rows_entry<P>(dst, src, p, lds); break;
     case kMoveGeneric: move_elements<P, 0>(dst, src, p); break;
     default: break;
   }
@@ -957,7 +1058,8 @@ template <typename P, int VL, int VS, int LA, int LB>
 __global__ void __launch_bounds__(kBlock)
     move_tile_once_kernel(void* dst, const void* src, TilePlan tp) {
   __shared__ P tile[LA * (LB + 1)];
-  move_tile_once<P, VL, VS, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src), tp, tile);
+  move_tile_once<P, VL, VS, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src), tp, tile,
+                                    blockIdx.x);
 }
 
 template <typename P, int BS>
