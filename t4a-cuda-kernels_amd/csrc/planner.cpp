@@ -690,6 +690,15 @@ int general_movement(int status, t4a_launch* launch) {
   return status;
 }
 
+// The same for the reduction twins (thread 0 fuses the geometry per block;
+// their loops stride over outputs and cubes): at most kAnyReduceBlocks blocks.
+constexpr unsigned kAnyReduceBlocks = 2048;
+
+void general_reduction(t4a_launch* launch) {
+  if (launch->variant == T4A_VARIANT_GENERAL && launch->grid[0] > kAnyReduceBlocks)
+    launch->grid[0] = kAnyReduceBlocks;
+}
+
 }  // namespace
 
 extern "C" {
@@ -936,8 +945,10 @@ int t4a_plan_reduce_any(int dtype, int op, int strategy, const t4a_cuda_layout_a
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_any(out_layout)) return s;
   if (int s = check_any(in_layout)) return s;
-  return plan_reduce(dtype, op, strategy, V(out_layout), out_len, V(in_layout), in_len, axis,
-                     plane_width, launch);
+  const int status = plan_reduce(dtype, op, strategy, V(out_layout), out_len, V(in_layout),
+                                 in_len, axis, plane_width, launch);
+  if (status == T4A_OK) general_reduction(launch);
+  return status;
 }
 
 // Reference plan_reduce_partials (src/lib.rs:3340-3431). A 32-lane plan runs
@@ -961,8 +972,10 @@ int t4a_plan_reduce_partials_any(int dtype, int op, const t4a_cuda_layout_any* p
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_any(partials_layout)) return s;
   if (int s = check_any(in_layout)) return s;
-  return plan_reduce_partials(dtype, op, V(partials_layout), partials_len, V(in_layout), in_len,
-                              axis, split, plane_width, launch);
+  const int status = plan_reduce_partials(dtype, op, V(partials_layout), partials_len,
+                                          V(in_layout), in_len, axis, split, plane_width, launch);
+  if (status == T4A_OK) general_reduction(launch);
+  return status;
 }
 
 // Reference plan_reduction (src/lib.rs:3457-3528) with combine_geometry and
@@ -986,8 +999,14 @@ int t4a_plan_reduction_any(int dtype, int op, const t4a_cuda_layout_any* out_lay
   std::memset(plan, 0, sizeof(*plan));
   if (int s = check_any(out_layout)) return s;
   if (int s = check_any(in_layout)) return s;
-  return plan_reduction(dtype, op, V(out_layout), out_len, V(in_layout), in_len, axis,
-                        plane_width, plan);
+  const int status = plan_reduction(dtype, op, V(out_layout), out_len, V(in_layout), in_len,
+                                    axis, plane_width, plan);
+  if (status == T4A_OK) {
+    general_reduction(&plan->launch);
+    general_reduction(&plan->pass1);
+    general_reduction(&plan->pass2);
+  }
+  return status;
 }
 
 // Reference reduction_partials_layout / partials_layout_for (src/lib.rs:3530-3557).

@@ -858,10 +858,21 @@ __device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const v
   const int planes = static_cast<int>(blockDim.x) / w;
   const int lane = static_cast<int>(threadIdx.x) % w;
   const long long cubes = output_len * splits;
-  for (long long cube = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
-       cube < cubes; cube += static_cast<long long>(gridDim.x) * planes) {
-    const long long o = cube / splits;
-    const long long split = cube - o * splits;
+  // Which cube a plane takes (never what it computes): on a contiguous axis
+  // neighbouring planes take neighbouring chunks of one output, which stream
+  // one run; on a strided axis they take neighbouring outputs of one split,
+  // so a block's planes read neighbouring columns of the same rows.
+  const bool split_major = rd.axis_stride != 1;
+  for (long long idx = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
+       idx < cubes; idx += static_cast<long long>(gridDim.x) * planes) {
+    long long o, split;
+    if (split_major) {
+      split = idx / output_len;
+      o = idx - split * output_len;
+    } else {
+      o = idx / splits;
+      split = idx - o * splits;
+    }
     long long ib, pb;
     decode_output(rd, o, &ib, &pb);
     pb += split * rd.out_axis_stride;
