@@ -21,9 +21,10 @@ reference algorithm restated in C, one thread) running whole steps of the same
 workload on the same inputs, repeated for about `--cpu-seconds`.
 
 Other workloads (--workload c1|c1big|c3|c4|c5) run the other benchmark configs
-the same way, `copy` the copy ceiling and `entries` the other movement entries
+the same way, `copy` the copy ceiling, `entries` the other movement entries
 (fill_zero, fill_zero_view, contiguous_to_view, broadcast_in_dim,
-concatenate_copy); they are for development, the driver's line is c2.
+concatenate_copy) and `general` the rank-9 `_any` twins; they are for
+development, the driver's line is c2.
 """
 from __future__ import annotations
 
@@ -394,7 +395,80 @@ def build_entries() -> Workload:
     return w
 
 
+def build_general() -> Workload:
+    """The general-rank twins at rank 9 (the benchmark layouts with extent-1 axes
+    appended, so the plans are GENERAL and fuse back to the rank <= 8 ones):
+    the C3 f64 and C5 c64 permutes, the 8192^2 f32 transpose, an f32 row copy,
+    and pass 1 of the C2 f32 sums over the inner and the outer axis, all with
+    their geometry in device memory."""
+    w = Workload("general", "rank-9 _any twins: C3 f64 / C5 c64 permutes, 8192^2 f32 "
+                 "transpose and row copy, C2 f32 inner / outer sum pass 1", "f64,c64,f32")
+    rng = np.random.default_rng(7)
+    keep = []  # device geometry arrays, alive for the workload's lifetime
+
+    def geometry(layout):
+        k = 9 - layout.rank
+        wide = t.WideLayout(layout.extents + [1] * k, layout.strides + [3] * k, layout.offset)
+        ext = hipmem.DeviceBuffer.from_array(np.array(wide.extents, dtype=np.int64))
+        st = hipmem.DeviceBuffer.from_array(np.array(wide.strides, dtype=np.int64))
+        keep.extend([ext, st])
+        return wide, wide.device_c(ext.ptr, st.ptr)
+
+    moves = [("permute4_F64", t.DType.F64,
+              t.Layout([64, 64, 128, 32], [32, 262144, -2048, 1], 260096)),
+             ("permute6_c64", t.DType.C64,
+              t.Layout([16] * 6, [256, 65536, 16, 1048576, 4096, 1], 0)),
+             ("transpose_f32_8192", t.DType.F32, t.Layout([8192, 8192], [8192, 1], 0)),
+             ("rows_f32_8192", t.DType.F32, t.Layout([8192, 8192], [1, 16384], 0))]
+    for name, dt, src_l in moves:
+        n = src_l.element_count()
+        span = src_l.max_reachable_offset() + 1
+        dst_l = t.Layout.compact(src_l.extents)
+        ws, cs = geometry(src_l)
+        wd, cd = geometry(dst_l)
+        plan = t.plan_strided_to_strided(dt, ws, span, wd, n)
+        host = rng.integers(0, 255, span * dt.size, dtype=np.uint8)
+        sets = _sets(host)
+        outs = [hipmem.DeviceBuffer(n * dt.size) for _ in range(ROTATE)]
+
+        def move(r, dt=dt, cs=cs, cd=cd, n=n, plan=plan, sets=sets, outs=outs):
+            hip.strided_to_strided_any(outs[r], sets[r], dt, cs, cd, n, plan, _stream())
+
+        w.ops.append(Op(f"{name}_any", "strided_to_strided_any", 2 * n * dt.size, move, move,
+                        2 * n * dt.size))
+    ext = [8192, 8192]
+    hf = rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32)
+    f = _sets(hf)
+    for name, axis in (("sum_f32_inner_pass1", 0), ("sum_f32_outer_pass1", 1)):
+        in_l = t.Layout.compact(ext)
+        oe = list(ext)
+        oe[axis] = 1
+        out_l = t.Layout.compact(oe)
+        n, on = in_l.element_count(), out_l.element_count()
+        rplan = t.plan_reduction(t.DType.F32, t.ReduceOp.Sum, out_l, on, in_l, n, axis, 32)
+        wi, ci = geometry(in_l)
+        wp = t.reduction_partials_layout(wi, axis, rplan.split.splits)
+        pe = hipmem.DeviceBuffer.from_array(np.array(wp.extents, dtype=np.int64))
+        ps = hipmem.DeviceBuffer.from_array(np.array(wp.strides, dtype=np.int64))
+        keep.extend([pe, ps])
+        cp = wp.device_c(pe.ptr, ps.ptr)
+        pn = wp.element_count()
+        p1 = t.plan_reduce_partials(t.DType.F32, t.ReduceOp.Sum, wp, pn, wi, n, axis,
+                                    rplan.split, 32)
+        part = hipmem.DeviceBuffer(pn * 4)
+
+        def pass1(r, cp=cp, ci=ci, axis=axis, on=on, rplan=rplan, p1=p1, part=part):
+            hip.reduce_partials_any(part, f[r], t.DType.F32, t.ReduceOp.Sum, cp, ci, axis, on,
+                                    rplan.split.splits, rplan.split.chunk_len, p1, _stream())
+
+        w.ops.append(Op(f"{name}_any", "reduce_partials_any", (n + pn) * 4, pass1, pass1,
+                        (n + pn) * 4))
+    w.keep = keep
+    return w
+
+
 WORKLOADS = {
+    "general": build_general,
     "entries": build_entries,
     "copy": build_copy,
     "c2": build_c2,
