@@ -870,6 +870,49 @@ struct PartialsPlan {
   long long units;      // blocks (TILES), planes (VECROWS), wavefronts (ROWS), cubes
 };
 
+// A reduction's layouts as a rank <= 8 pair with the same fused dims (for
+// partials_plan): the layouts themselves up to rank 8, else the non-axis dims
+// fused (reduce_dims_view) with the axis appended last. False when more than
+// seven non-axis dims remain. Arrays may be host or device memory.
+T4A_HD bool reduction_pair_view(int rank, long long out_offset, const long long* out_ext,
+                                const long long* out_str, long long in_offset,
+                                const long long* in_ext, const long long* in_str, int axis,
+                                t4a_cuda_layout* o8, t4a_cuda_layout* i8, int* axis8) {
+  o8->rank = i8->rank = 0;
+  o8->offset = out_offset;
+  i8->offset = in_offset;
+  for (int k = 0; k < kMaxDims; ++k) {
+    o8->extents[k] = o8->strides[k] = i8->extents[k] = i8->strides[k] = 0;
+  }
+  if (rank <= kMaxDims) {
+    o8->rank = i8->rank = rank;
+    for (int k = 0; k < rank; ++k) {
+      o8->extents[k] = out_ext[k];
+      o8->strides[k] = out_str[k];
+      i8->extents[k] = in_ext[k];
+      i8->strides[k] = in_str[k];
+    }
+    *axis8 = axis;
+    return true;
+  }
+  ReduceDimsN<kMaxDims - 1> rd;
+  if (!reduce_dims_view(&rd, rank, axis, out_offset, out_ext, out_str, in_offset, in_ext,
+                        in_str))
+    return false;
+  o8->rank = i8->rank = rd.n + 1;
+  for (int k = 0; k < rd.n; ++k) {
+    o8->extents[k] = i8->extents[k] = rd.ext[k];
+    o8->strides[k] = rd.os[k];
+    i8->strides[k] = rd.is[k];
+  }
+  o8->extents[rd.n] = out_ext[axis];
+  o8->strides[rd.n] = out_str[axis];
+  i8->extents[rd.n] = in_ext[axis];
+  i8->strides[rd.n] = in_str[axis];
+  *axis8 = rd.n;
+  return true;
+}
+
 // `align`: the input pointer's alignment in bytes (the planner, which has no
 // pointer, assumes 16; the launcher passes the real one). A plan made for a
 // better-aligned pointer still runs correctly through the launcher, which

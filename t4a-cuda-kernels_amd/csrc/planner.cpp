@@ -370,40 +370,8 @@ int plan_strided(int dtype, const View& src, long long src_len, const View& dst,
 // reproduces those dims. False when more than 7 non-axis dims remain.
 bool reduction_pair(const View& out, const View& in, unsigned axis, t4a_cuda_layout* o8,
                     t4a_cuda_layout* i8, int* axis8) {
-  std::memset(o8, 0, sizeof(*o8));
-  std::memset(i8, 0, sizeof(*i8));
-  if (in.rank <= T4A_CUDA_MAX_RANK) {
-    o8->rank = out.rank;
-    i8->rank = in.rank;
-    o8->offset = out.offset;
-    i8->offset = in.offset;
-    for (int k = 0; k < in.rank; ++k) {
-      o8->extents[k] = out.extents[k];
-      o8->strides[k] = out.strides[k];
-      i8->extents[k] = in.extents[k];
-      i8->strides[k] = in.strides[k];
-    }
-    *axis8 = static_cast<int>(axis);
-    return true;
-  }
-  t4a::ReduceDimsN<T4A_CUDA_MAX_RANK - 1> rd;
-  if (!t4a::reduce_dims_view(&rd, in.rank, static_cast<int>(axis), out.offset, out.extents,
-                             out.strides, in.offset, in.extents, in.strides))
-    return false;
-  o8->rank = i8->rank = rd.n + 1;
-  o8->offset = out.offset;
-  i8->offset = in.offset;
-  for (int k = 0; k < rd.n; ++k) {
-    o8->extents[k] = i8->extents[k] = rd.ext[k];
-    o8->strides[k] = rd.os[k];
-    i8->strides[k] = rd.is[k];
-  }
-  o8->extents[rd.n] = out.extents[axis];
-  o8->strides[rd.n] = out.strides[axis];
-  i8->extents[rd.n] = in.extents[axis];
-  i8->strides[rd.n] = in.strides[axis];
-  *axis8 = rd.n;
-  return true;
+  return t4a::reduction_pair_view(in.rank, out.offset, out.extents, out.strides, in.offset,
+                                  in.extents, in.strides, static_cast<int>(axis), o8, i8, axis8);
 }
 
 // Reference plan_reduce (src/lib.rs:3318-3338) with check_reduce_width and

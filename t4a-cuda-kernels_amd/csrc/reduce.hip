@@ -1263,6 +1263,21 @@ __device__ __forceinline__ void dispatch_fold(int op, Fn&& fn) {
   }
 }
 
+// A value every lane holds alike, read out of LDS into scalar registers (one
+// readfirstlane per dword), so that a loop reads it without LDS traffic.
+template <typename T>
+__device__ __forceinline__ T uniform_copy(const T& shared_value) {
+  static_assert(sizeof(T) % 4 == 0, "whole dwords");
+  unsigned int words[sizeof(T) / 4];
+  __builtin_memcpy(words, &shared_value, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(T) / 4); ++i)
+    words[i] = __builtin_amdgcn_readfirstlane(words[i]);
+  T out;
+  __builtin_memcpy(&out, words, sizeof(T));
+  return out;
+}
+
 template <typename Fn>
 __device__ __forceinline__ void dispatch_dtype(int dtype, Fn&& fn) {
   switch (dtype) {
@@ -1461,15 +1476,74 @@ extern "C" __global__ void __launch_bounds__(512)
   });
 }
 
+// The launchers' column mapping for a general-rank pass 1 (a strided axis
+// with neighbouring output columns): thread 0 rebuilds the rank <= 8 layout
+// pair the host planner plans with (reduction_pair_view), plans pass 1 as the
+// by-value launcher does, and keeps the SidePlan when that plan is TILES
+// (returning its columns per lane, 0 otherwise).
+__device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, int dtype, const void* in,
+                                             const t4a_cuda_layout_any& partials,
+                                             const t4a_cuda_layout_any& input, int axis,
+                                             long long output_len, long long splits,
+                                             long long chunk_len) {
+  if (!t4a::sideways_dtype(dtype) || axis < 0 || axis >= input.rank ||
+      partials.rank != input.rank)
+    return 0;
+  t4a_cuda_layout p8, i8;
+  int axis8;
+  if (!t4a::reduction_pair_view(input.rank, partials.offset, partials.extents, partials.strides,
+                                input.offset, input.extents, input.strides, axis, &p8, &i8,
+                                &axis8))
+    return 0;
+  const uintptr_t address = reinterpret_cast<uintptr_t>(in);
+  const int align = (address & 15) == 0 ? 16 : (address & 7) == 0 ? 8 : (address & 3) == 0 ? 4 : 1;
+  t4a::PartialsPlan pp;
+  t4a::partials_plan(&pp, p8, i8, axis8, output_len, splits, t4a::kWarp, 1,
+                     t4a::dtype_size(dtype), align);
+  if (pp.mode != t4a::kPartialsTiles) return 0;
+  *side = t4a::side_plan(pp, splits, chunk_len);
+  return pp.cpl;
+}
+
 extern "C" __global__ void __launch_bounds__(256)
     t4a_cuda_reduce_partials_any(void* partials, const void* in, int dtype, int op,
                                  t4a_cuda_layout_any partials_layout,
                                  t4a_cuda_layout_any in_layout, int axis, long long output_len,
                                  long long splits, long long chunk_len) {
   __shared__ t4a::ReduceDimsWide rd;
-  if (threadIdx.x == 0) any_dims(&rd, partials_layout, in_layout, axis);
+  __shared__ t4a::SidePlan side;
+  __shared__ int side_cpl;
+  __shared__ alignas(16) unsigned char tiles_lds[(t4a::kBlock / t4a::kWave) * t4a::kWave * 2 * 8];
+  __shared__ int redo;
+  const bool whole_waves = blockDim.x == static_cast<unsigned>(t4a::kBlock) &&
+                           blockDim.y == 1 && blockDim.z == 1;
+  if (threadIdx.x == 0) {
+    any_dims(&rd, partials_layout, in_layout, axis);
+    // Only a strided axis can take the column mapping.
+    side_cpl = rd.n >= 0 && whole_waves && rd.axis_stride != 1
+                   ? any_side_plan(&side, dtype, in, partials_layout, in_layout, axis,
+                                   output_len, splits, chunk_len)
+                   : 0;
+  }
   __syncthreads();
   if (rd.n < 0) return;
+  if (side_cpl > 0) {
+    const t4a::SidePlan sp = t4a::uniform_copy(side);
+    const int cpl = side_cpl;
+    t4a::dispatch_dtype(dtype, [&](auto* tag) {
+      using T = std::remove_pointer_t<decltype(tag)>;
+      if constexpr (t4a::VecLanes<T>::value > 0) {
+        T* lds = reinterpret_cast<T*>(tiles_lds);
+        t4a::dispatch_fold<T>(op, [&](auto fold) {
+          if (cpl == 2)
+            t4a::partials_tiles<decltype(fold), T, 2>(partials, in, sp, fold, lds, &redo);
+          else
+            t4a::partials_tiles<decltype(fold), T, 1>(partials, in, sp, fold, lds, &redo);
+        });
+      }
+    });
+    return;
+  }
   t4a::dispatch_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
     t4a::dispatch_fold<T>(op, [&](auto fold) {

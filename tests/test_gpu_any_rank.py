@@ -356,3 +356,54 @@ def test_rank_nine_split_reaches_every_partial_through_the_wide_combine():
     hip.enqueue_reduction(fplan, fout, d_src, fpart, F32, ReduceOp.Max, fo, fi, 1, on, stream())
     assert np.array_equal(to_host(fpart, pn * 4), to_host(part, pn * 4))
     assert np.array_equal(to_host(fout, on * 4), to_host(out, on * 4))
+
+
+@pytest.mark.parametrize("dtype", [F32, F64, DType.I32, DType.I64], ids=lambda d: d.name)
+def test_strided_axis_pass1_twin_takes_the_column_mapping(dtype):
+    """A pass 1 over a strided axis with neighbouring output columns: the twin
+    plans the launchers' column mapping inside the kernel. At rank 9 (extent-1
+    axes appended: a GENERAL plan) and rank 3 through the twin, its partials are
+    the by-value launcher's and the oracle's bytes, for every op the dtype has,
+    full and ragged column blocks, aligned and shifted inputs."""
+    rng = np.random.default_rng(90)
+    ops = [ReduceOp.Sum, ReduceOp.Max, ReduceOp.Min, ReduceOp.Prod]
+    if dtype in (F32, F64):
+        ops.append(ReduceOp.SumSquares)
+    for cols, rows, other, shift in ((256, 1024, 1, 0), (300, 768, 2, 0), (129, 512, 1, 1)):
+        ext = [cols, rows, other]
+        axis = 1
+        n = count(ext)
+        if dtype in (DType.I32, DType.I64):
+            src = rng.integers(-3, 4, n + shift).astype(NUMPY[dtype])
+        else:
+            src = rng.uniform(-1, 1, n + shift).astype(NUMPY[dtype])
+        d_src = to_device(src)
+        fi = Layout([cols, rows, other], [1, cols, cols * rows], shift)
+        out_ext = [cols, 1, other]
+        fo = Layout.compact(out_ext)
+        on = count(out_ext)
+        split = t.split_policy(rows, 32)
+        pl = t.reduction_partials_layout(Layout.compact(ext), axis, split.splits)
+        pn = pl.element_count()
+        for rank in (3, 9):
+            k = rank - 3
+            wi = WideLayout(ext + [1] * k, fi.strides + [5] * k, shift)
+            wp = WideLayout(pl.extents + [1] * k, pl.strides + [5] * k, 0)
+            gi, gp = Geometry(wi), Geometry(wp)
+            for op in ops:
+                plan = t.plan_reduce_partials(dtype, op, pl, pn, fi, n + shift, axis, split, 32)
+                aplan = t.plan_reduce_partials(dtype, op, wp, pn, wi, n + shift, axis, split, 32)
+                if rank == 9:
+                    assert aplan.variant == t.RankVariant.General
+                say("strided pass-1 twin", dtype.name, ext, shift, rank, op.name, aplan.grid)
+                a, b = sentinel(pn * dtype.size), sentinel(pn * dtype.size)
+                hip.reduce_partials(a, d_src, dtype, op, pl, fi, axis, on, split.splits,
+                                    split.chunk_len, plan, stream())
+                hip.reduce_partials_any(b, d_src, dtype, op, gp.c, gi.c, axis, on, split.splits,
+                                        split.chunk_len, aplan, stream())
+                want = np.zeros(pn, dtype=NUMPY[dtype])
+                orc.reduce_partials(want, src, dtype, op, 32, pl, fi, axis, on, split.splits,
+                                    split.chunk_len)
+                ga, gb = to_host(a, pn * dtype.size), to_host(b, pn * dtype.size)
+                assert np.array_equal(gb, ga), (ext, shift, rank, op)
+                assert np.array_equal(ga, want.view(np.uint8)), (ext, shift, rank, op)
