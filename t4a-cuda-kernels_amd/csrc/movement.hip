@@ -378,7 +378,11 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
 // dst_b(j), the chain offsets decoded per slot (at most two digits). A partial
 // tile's empty slots load the tile's first element instead (so no branch
 // separates the loads) and are neither parked nor stored.
-template <typename P, int VL, int VS, int LA, int LB>
+// `Walk`: the tile is `tile_index` (the entries' tile loop); otherwise
+// blockIdx.x, read directly (the launchers' kernel: taking it as an argument
+// changed the store loop's register allocation so that every LDS read waited
+// for all earlier stores, 4 % slower on C3).
+template <typename P, int VL, int VS, int LA, int LB, bool Walk = false>
 __device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __restrict__ src,
                                                const TilePlan& tp, P* tile,
                                                unsigned int tile_index) {
@@ -389,7 +393,7 @@ __device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __r
   constexpr int RL = LA * LBV / BS;
   constexpr int RS = LB * LAV / BS;
   static_assert(RL * BS == LA * LBV && RS * BS == LB * LAV, "the block divides the tile");
-  unsigned int rest = tile_index;
+  unsigned int rest = Walk ? tile_index : blockIdx.x;
   unsigned int first = 0, ta = 0, tb = 0;
   long long sb = tp.src_offset;
   long long db = tp.dst_offset;
@@ -675,8 +679,8 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
           constexpr int VLt = decltype(vl_tag)::value;
           constexpr int VSt = decltype(vs_tag)::value;
           for (unsigned int t = blockIdx.x; t < tiles; t += gridDim.x) {
-            move_tile_once<P, VLt, VSt, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src),
-                                                tp, tile, t);
+            move_tile_once<P, VLt, VSt, LA, LB, true>(static_cast<P*>(dst),
+                                                      static_cast<const P*>(src), tp, tile, t);
             __syncthreads();  // the tile's LDS is rewritten by the next one
           }
         };
@@ -1059,7 +1063,7 @@ __global__ void __launch_bounds__(kBlock)
     move_tile_once_kernel(void* dst, const void* src, TilePlan tp) {
   __shared__ P tile[LA * (LB + 1)];
   move_tile_once<P, VL, VS, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src), tp, tile,
-                                    blockIdx.x);
+                                    0);
 }
 
 template <typename P, int BS>
