@@ -21,7 +21,8 @@ reference algorithm restated in C, one thread) running whole steps of the same
 workload on the same inputs, repeated for about `--cpu-seconds`.
 
 Other workloads (--workload c1|c1big|c3|c4|c5) run the other benchmark configs
-the same way, `copy` the copy ceiling, `entries` the other movement entries
+the same way, `c1graph` C1's transposes replayed as one HIP graph, `copy` the
+copy ceiling, `entries` the other movement entries
 (fill_zero, fill_zero_view, contiguous_to_view, broadcast_in_dim,
 concatenate_copy) and `general` the rank-9 `_any` twins; they are for
 development, the driver's line is c2.
@@ -259,6 +260,34 @@ def build_c1(m: int) -> Workload:
     return w
 
 
+def build_c1_graph(m: int, count: int = 100) -> Workload:
+    """C1's transposes captured into one HIP graph: `count` launches over the
+    rotating sets per replay, so the per-launch cost of a small transpose is
+    the graph's, not one submission's."""
+    w = Workload(f"c1graph-{m}", f"C1: {count} tiled transposes f32 [{m},{m}] (1,0) replayed "
+                 "as one HIP graph", "f32")
+    host = np.random.default_rng(0).uniform(-1.0, 1.0, m * m).astype(np.float32)
+    sets = _sets(host)
+    outs = _empty_like(sets)
+    dt = t.DType.F32
+    cfg = t.TransposeConfig.DEFAULT
+    plan = t.plan_tiled_transpose(dt, cfg, 0, m * m, m, m, 1, m * m, m * m)
+    s = _stream()
+
+    def record():
+        for i in range(count):
+            r = i % ROTATE
+            hip.tiled_transpose(outs[r], sets[r], dt, 0, m * m, m, m, cfg, plan, s)
+
+    graph = hipmem.Graph(s, record)
+    w.keep = [graph, sets, outs]
+    replay = lambda r: graph.launch(s)  # noqa: E731
+    nbytes = 2 * m * m * dt.size * count
+    w.ops.append(Op(f"transpose_f32_{m}_x{count}_graph", "tiled_transpose (graph)", nbytes,
+                    replay, replay, nbytes))
+    return w
+
+
 def build_c3() -> Workload:
     w = Workload("c3", "C3: strided_to_strided C-[64,128,64,32] perm (3,1,0,2), reversed "
                  "axis, f64 and c32", "f64,c32")
@@ -474,6 +503,7 @@ WORKLOADS = {
     "c2": build_c2,
     "c1": lambda: build_c1(1024),
     "c1big": lambda: build_c1(8192),
+    "c1graph": lambda: build_c1_graph(1024),
     "c3": build_c3,
     "c4": build_c4,
     "c5": build_c5,

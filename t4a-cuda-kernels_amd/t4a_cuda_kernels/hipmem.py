@@ -50,6 +50,13 @@ def hip() -> ctypes.CDLL:
                                               ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
                                               ctypes.c_uint, ctypes.c_uint, c_void_p,
                                               ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]
+        lib.hipStreamBeginCapture.argtypes = [c_void_p, c_int]
+        lib.hipStreamEndCapture.argtypes = [c_void_p, ctypes.POINTER(c_void_p)]
+        lib.hipGraphInstantiate.argtypes = [ctypes.POINTER(c_void_p), c_void_p, c_void_p,
+                                            ctypes.c_char_p, c_size_t]
+        lib.hipGraphLaunch.argtypes = [c_void_p, c_void_p]
+        lib.hipGraphExecDestroy.argtypes = [c_void_p]
+        lib.hipGraphDestroy.argtypes = [c_void_p]
         _HIP = lib
     return _HIP
 
@@ -154,6 +161,50 @@ class Stream:
         try:
             if self.handle:
                 hip().hipStreamDestroy(c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+class Graph:
+    """The launches `record()` enqueues on `stream`, captured once into a HIP
+    graph (hipStreamBeginCapture / hipStreamEndCapture, thread-local mode) and
+    instantiated; `launch()` replays them with one submission. The library's
+    launchers allocate nothing and record no memsets, so they capture as they
+    run; a replay reads and writes the buffers the capture named."""
+
+    _THREAD_LOCAL = 1  # hipStreamCaptureModeThreadLocal
+
+    def __init__(self, stream: "Stream", record):
+        lib = hip()
+        check(lib.hipStreamBeginCapture(c_void_p(stream.handle), self._THREAD_LOCAL),
+              "hipStreamBeginCapture")
+        g = c_void_p()
+        try:
+            record()
+        finally:
+            status = lib.hipStreamEndCapture(c_void_p(stream.handle), byref(g))
+        check(status, "hipStreamEndCapture")
+        self._graph = g.value
+        e = c_void_p()
+        check(lib.hipGraphInstantiate(byref(e), c_void_p(self._graph), None, None, 0),
+              "hipGraphInstantiate")
+        self._exec = e.value
+
+    def launch(self, stream: "Stream") -> None:
+        check(hip().hipGraphLaunch(c_void_p(self._exec), c_void_p(stream.handle)),
+              "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if getattr(self, "_exec", None):
+            hip().hipGraphExecDestroy(c_void_p(self._exec))
+            self._exec = None
+        if getattr(self, "_graph", None):
+            hip().hipGraphDestroy(c_void_p(self._graph))
+            self._graph = None
+
+    def __del__(self):
+        try:
+            self.destroy()
         except Exception:
             pass
 
