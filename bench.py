@@ -8,7 +8,10 @@ i64 sum over the inner axis, each a planned reduction (pass 1 + combine)
 launched through the C ABI. One step = those five reductions over one input
 set. Inputs are resident in HBM before timing; three input sets rotate so a
 step never finds its input in the 256 MB Infinity Cache left by the previous
-step.
+step. The step is launched one call at a time (`"launch": "eager"`); with
+`--graph` it is captured once per input set into a HIP graph and replayed
+(`"launch": "hip_graph"`, each graph's output bytes checked against the eager
+step's before timing), and `"eager"` keeps the eager figure beside it.
 
 Effective bytes = logical input bytes read once + logical output bytes written
 once (partials excluded), 1 GB = 1e9 B. `roofline` is the dominant kernel's
@@ -95,6 +98,9 @@ class Op:
     dominant: Callable[[int], None]  # enqueue only the dominant kernel
     dominant_bytes: int              # algorithmic bytes of the dominant kernel
     cpu: Callable[[], None] | None = None  # the same op through the CPU oracle
+    # the buffers the op writes on set r, as (buffer, bytes): lets a captured
+    # step be checked against the eager one
+    outputs: Callable[[int], list] | None = None
 
 
 @dataclass
@@ -191,7 +197,9 @@ def reduction_op(name, dtype, op, in_ext, axis, sets, host) -> Op:
         kernel, dom_bytes = "reduce_partials", (n + pl.element_count()) * es
     else:
         kernel, dom_bytes = "reduce", (n + on) * es
-    return Op(name, kernel, (n + on) * es, launch, dominant, dom_bytes, cpu)
+    written = [(out, on * es)] + ([(part, pl.element_count() * es)] if part is not None else [])
+    return Op(name, kernel, (n + on) * es, launch, dominant, dom_bytes, cpu,
+              lambda r: written)
 
 
 def transpose_op(name, dtype, m, n, sets, outs, host) -> Op:
@@ -210,7 +218,7 @@ def transpose_op(name, dtype, m, n, sets, outs, host) -> Op:
         _oracle().tiled_transpose(h_dst[0], host, dtype, 0, m * n, m, n, 1)
 
     return Op(name, "tiled_transpose", 2 * m * n * dtype.size, launch, launch,
-              2 * m * n * dtype.size, cpu)
+              2 * m * n * dtype.size, cpu, lambda r: [(outs[r], m * n * dtype.size)])
 
 
 def move_op(name, dtype, src_l, dst_l, sets, outs, host) -> Op:
@@ -230,7 +238,7 @@ def move_op(name, dtype, src_l, dst_l, sets, outs, host) -> Op:
         _oracle().strided_to_strided(h_dst[0], host, dtype, src_l, dst_l, count)
 
     return Op(name, "strided_to_strided", 2 * count * dtype.size, launch, launch,
-              2 * count * dtype.size, cpu)
+              2 * count * dtype.size, cpu, lambda r: [(outs[r], dst_len * dtype.size)])
 
 
 # ---- workloads ---------------------------------------------------------------------
@@ -524,6 +532,31 @@ def time_ops(fn: Callable[[int], None], count: int) -> float:
     return start.elapsed_ms(stop) / count
 
 
+def captured_steps(w: Workload, step: Callable[[int], None]) -> list:
+    """One HIP graph per buffer set holding the whole step's launches. Each is
+    checked once before it is timed: the eager step's output bytes are kept,
+    the outputs refilled with a sentinel, and one replay must write the same
+    bytes (partials included)."""
+    s = _stream()
+    graphs = []
+    for r in range(ROTATE):
+        g = hipmem.Graph(s, lambda r=r: step(r))
+        step(r)
+        s.synchronize()
+        bufs = [b for op in w.ops for b in op.outputs(r)]
+        want = [buf.download(n) for buf, n in bufs]
+        for buf, _ in bufs:
+            buf.fill(0xCD)
+        g.launch(s)
+        s.synchronize()
+        for (buf, n), x in zip(bufs, want):
+            if not np.array_equal(buf.download(n), x):
+                sys.exit(f"bench.py: the captured step of set {r} wrote other bytes than the "
+                         f"eager step")
+        graphs.append(g)
+    return graphs
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -536,6 +569,9 @@ def main() -> None:
     ap.add_argument("--kernel-only", metavar="OP",
                     help="launch only OP's dominant kernel, warmup + steps times (for "
                          "rocprofv3 counter passes), and print one line")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the step captured once per input set into a HIP graph and "
+                         "replayed (checked against the eager step first)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
@@ -564,8 +600,17 @@ def main() -> None:
     for i in range(args.warmup):
         step(i % ROTATE)
     _stream().synchronize()
-    ms_per_step = time_ops(step, args.steps)
     step_bytes = sum(op.algo_bytes for op in w.ops)
+    eager_ms = time_ops(step, args.steps)
+    launch_mode, ms_per_step = "eager", eager_ms
+    if args.graph and all(op.outputs is not None for op in w.ops):
+        graphs = captured_steps(w, step)
+        replay = lambda r: graphs[r].launch(_stream())  # noqa: E731
+        for i in range(args.warmup):
+            replay(i % ROTATE)
+        _stream().synchronize()
+        ms_per_step = time_ops(replay, args.steps)
+        launch_mode = "hip_graph"
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # Per-op and dominant-kernel timings (same stream, same rotation).
@@ -619,6 +664,9 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "launch": launch_mode,
+        "eager": {"ms_per_step": round(eager_ms, 5),
+                  "value": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
