@@ -362,12 +362,17 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
     unit_decode(up, o, &ib, &ob);
     const T* x = in + ib;
     T acc;
-    constexpr int kShort = 32;
-    if (BS != kBlock && len <= kShort) {
+    // A short axis takes every load before the first fold: the combine passes
+    // (up to 32 partials), and in the large grids up to 16 elements (the c64
+    // [16]^6 sum over a stride-256 axis), whose wavefronts otherwise wait on
+    // each group of four loads in turn.
+    constexpr int kShort = BS != kBlock ? 32 : 16;
+    if (len <= kShort) {
       T v[kShort];
 #pragma unroll
       for (int k = 0; k < kShort; ++k) {
-        if (k < len) v[k] = x[k * stride];
+        // the large grids read their input once: streaming loads
+        if (k < len) v[k] = BS == kBlock ? nt_load<T, 1>(x + k * stride).v[0] : x[k * stride];
       }
       acc = f.seed(v[0]);
 #pragma unroll
@@ -379,7 +384,10 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
 #pragma unroll 4
       for (int i = 1; i < len; ++i) acc = f.fold(acc, x[i * stride]);
     }
-    out[ob] = acc;
+    if constexpr (BS == kBlock)
+      nt_store<T, 1>(out + ob, Vec<T, 1>{{acc}});
+    else
+      out[ob] = acc;
   }
 }
 
