@@ -6,9 +6,19 @@
 #include "t4a_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Threads for the loops over independent outputs (the all-core CPU baseline);
+ * 1 unless set. Every output's fold stays one serial loop on one thread, so
+ * no result depends on the count. */
+static int g_threads = 1;
+
+void t4a_oracle_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+
+int t4a_oracle_max_threads(void) { return omp_get_max_threads(); }
 
 int t4a_oracle_dtype_size(int dtype) {
   switch (dtype) {
@@ -44,6 +54,7 @@ void t4a_oracle_materialize_strided(void* dst, const void* src, int dtype,
   if (es == 0) return; /* unknown tag: no work (c-kernel-abi.md:107-108) */
   unsigned char* d = (unsigned char*)dst;
   const unsigned char* s = (const unsigned char*)src;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (long long f = 0; f < len; ++f) {
     const long long index = decode(f, l->rank, l->extents, l->strides, l->offset);
     memcpy(d + f * es, s + index * es, (size_t)es);
@@ -57,6 +68,7 @@ void t4a_oracle_strided_to_strided(void* dst, const void* src, int dtype,
   if (es == 0) return;
   unsigned char* d = (unsigned char*)dst;
   const unsigned char* s = (const unsigned char*)src;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (long long f = 0; f < len; ++f) {
     const long long si = decode(f, sl->rank, sl->extents, sl->strides, sl->offset);
     /* Both layouts share the source's extents (movement.cu:139-141). */
@@ -144,6 +156,7 @@ void t4a_oracle_tiled_transpose(void* dst, const void* src, int dtype, long long
   if (es == 0) return;
   unsigned char* d = (unsigned char*)dst;
   const unsigned char* s = (const unsigned char*)src;
+#pragma omp parallel for collapse(2) num_threads(g_threads) schedule(static)
   for (long long b = 0; b < batches; ++b) {
     for (long long i = 0; i < m; ++i) {
       for (long long j = 0; j < n; ++j) {
@@ -387,6 +400,7 @@ static void reduce_offsets(const t4a_cuda_layout* out, const t4a_cuda_layout* in
   do {                                                                                     \
     const T* src = (const T*)in;                                                           \
     T* dst = (T*)out;                                                                      \
+    _Pragma("omp parallel for num_threads(g_threads) schedule(static)")                    \
     for (long long o = 0; o < output_len; ++o) {                                           \
       long long base, off;                                                                 \
       reduce_offsets(out_layout, in_layout, o, &base, &off);                               \
@@ -421,8 +435,9 @@ void t4a_oracle_reduce(void* out, const void* in, int dtype, int op, int strateg
   do {                                                                                     \
     const T* src = (const T*)in;                                                           \
     T* dst = (T*)partials;                                                                 \
-    T lanes[32];                                                                           \
+    _Pragma("omp parallel for num_threads(g_threads) schedule(static)")                    \
     for (long long cube = 0; cube < output_len * splits; ++cube) {                         \
+      T lanes[32];                                                                         \
       const long long o = cube / splits, split = cube % splits;                            \
       long long base = in_layout->offset, poff = partials_layout->offset, rest = o;        \
       for (int d = 0; d < partials_layout->rank; ++d) {                                    \

@@ -95,6 +95,11 @@ unsigned long long t4a_oracle_fnv1a64(const void* bytes, unsigned long long len)
 /* Bytes per element of a dtype tag, 0 for an unknown tag. */
 int t4a_oracle_dtype_size(int dtype);
 
+/* Threads for the movement and reduction loops (OpenMP over independent
+ * outputs; results do not depend on it). Default 1. */
+void t4a_oracle_set_threads(int n);
+int t4a_oracle_max_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,10 @@ def load() -> ctypes.CDLL:
         lib.t4a_oracle_fnv1a64.restype = ctypes.c_ulonglong
         lib.t4a_oracle_dtype_size.argtypes = [c_int]
         lib.t4a_oracle_dtype_size.restype = c_int
+        lib.t4a_oracle_set_threads.argtypes = [c_int]
+        lib.t4a_oracle_set_threads.restype = None
+        lib.t4a_oracle_max_threads.argtypes = []
+        lib.t4a_oracle_max_threads.restype = c_int
         for name in ("t4a_oracle_fill_zero_view", "t4a_oracle_contiguous_to_view",
                      "t4a_oracle_broadcast_in_dim", "t4a_oracle_concatenate_copy"):
             getattr(lib, name).restype = None
@@ -132,6 +136,16 @@ def reduce_f64(inp: np.ndarray, dtype: int, op: int, in_layout, axis: int,
     load().t4a_oracle_reduce_f64(out.ctypes.data_as(POINTER(c_double)), _p(inp), int(dtype),
                                  int(op), _l(in_layout), axis, output_len)
     return out
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads for the loops over independent outputs (default 1);
+    every output is still folded serially on one thread."""
+    load().t4a_oracle_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(load().t4a_oracle_max_threads())
 
 
 def fnv1a64(a: np.ndarray) -> int:
