@@ -649,7 +649,10 @@ int plan_concatenate(int dtype, const View& out, long long out_len, const View& 
 // move plan): at most kAnyMoveBlocks persistent blocks, so that each block
 // plans once and then strides over many tiles, rows or elements (one block
 // per tile measured 3-4x slower, every block paying the serial planning).
-constexpr unsigned kAnyMoveBlocks = 1024;
+// Rank-9 versions of the benchmark movements measured best at 512 blocks (two
+// per CU): 4.1-5.0 TB/s, against 3.0-4.2 at 256, 3.6-4.7 at 1024 and 2.7-4.2
+// at 2048.
+constexpr unsigned kAnyMoveBlocks = 512;
 
 int general_movement(int status, t4a_launch* launch) {
   if (status == T4A_OK && launch->variant == T4A_VARIANT_GENERAL &&
@@ -659,12 +662,22 @@ int general_movement(int status, t4a_launch* launch) {
 }
 
 // The same for the reduction twins (thread 0 fuses the geometry per block;
-// their loops stride over outputs and cubes): at most kAnyReduceBlocks blocks.
-constexpr unsigned kAnyReduceBlocks = 2048;
+// their loops stride over outputs and cubes). Pass 1 over a strided axis, where
+// a block may take the column tiles, measured best at 512 blocks (rank-9 f32:
+// 4.8 TB/s, against 4.5 at 1024 and 3.8 at 2048); over a contiguous axis, the
+// plane mapping over short cubes, at 1024 (4.0 TB/s, against 2.5 at 512 and
+// 3.9 at 2048). Direct reductions and the combine keep 1024.
+constexpr unsigned kAnyReduceBlocks = 1024;
+constexpr unsigned kAnyPass1StridedBlocks = 512;
 
-void general_reduction(t4a_launch* launch) {
-  if (launch->variant == T4A_VARIANT_GENERAL && launch->grid[0] > kAnyReduceBlocks)
-    launch->grid[0] = kAnyReduceBlocks;
+void general_reduction(t4a_launch* launch, unsigned cap = kAnyReduceBlocks) {
+  if (launch->variant == T4A_VARIANT_GENERAL && launch->grid[0] > cap) launch->grid[0] = cap;
+}
+
+// The pass-1 cap for reducing `axis` of `in` (a checked layout, axis < rank).
+unsigned pass1_blocks(const t4a_cuda_layout_any* in, unsigned int axis) {
+  const long long stride = V(in).strides[axis];
+  return stride == 1 || stride == -1 ? kAnyReduceBlocks : kAnyPass1StridedBlocks;
 }
 
 }  // namespace
@@ -942,7 +955,7 @@ int t4a_plan_reduce_partials_any(int dtype, int op, const t4a_cuda_layout_any* p
   if (int s = check_any(in_layout)) return s;
   const int status = plan_reduce_partials(dtype, op, V(partials_layout), partials_len,
                                           V(in_layout), in_len, axis, split, plane_width, launch);
-  if (status == T4A_OK) general_reduction(launch);
+  if (status == T4A_OK) general_reduction(launch, pass1_blocks(in_layout, axis));
   return status;
 }
 
@@ -971,7 +984,7 @@ int t4a_plan_reduction_any(int dtype, int op, const t4a_cuda_layout_any* out_lay
                                     axis, plane_width, plan);
   if (status == T4A_OK) {
     general_reduction(&plan->launch);
-    general_reduction(&plan->pass1);
+    general_reduction(&plan->pass1, pass1_blocks(in_layout, axis));
     general_reduction(&plan->pass2);
   }
   return status;
