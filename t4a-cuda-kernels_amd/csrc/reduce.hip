@@ -274,6 +274,12 @@ __device__ __forceinline__ void unit_decode(const UnitPlan& up, unsigned int o, 
   *ob = w;
 }
 
+// The plane body's decode on a compact plan (output indices below 2^31).
+__device__ __forceinline__ void decode_output(const UnitPlan& up, long long o, long long* ib,
+                                              long long* ob) {
+  unit_decode(up, static_cast<unsigned int>(o), ib, ob);
+}
+
 template <typename Fold, typename T, int BS>
 __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restrict__ in,
                                           const UnitPlan& up, unsigned int output_len, Fold f) {
@@ -410,9 +416,28 @@ __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, co
     long long ib, ob;
     decode_output(rd, o, &ib, &ob);
     const T* x = in + ib;
-    T acc = f.seed(x[lane * stride]);
+    T acc;
+    // A plane holds len >= w elements. When a lane walks at most kAhead of them
+    // (the combine passes: 8 partials a lane for 4096 splits at W = 512), every
+    // load is issued before the first fold, one memory round trip per output.
+    constexpr int kAhead = 16;
+    if (len <= static_cast<long long>(w) * kAhead) {
+      T v[kAhead];
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) {
+        const long long i = lane + static_cast<long long>(k) * w;
+        if (i < len) v[k] = x[i * stride];
+      }
+      acc = f.seed(v[0]);
+#pragma unroll
+      for (int k = 1; k < kAhead; ++k) {
+        if (lane + static_cast<long long>(k) * w < len) acc = f.fold(acc, v[k]);
+      }
+    } else {
+      acc = f.seed(x[lane * stride]);
 #pragma unroll 4
-    for (long long i = lane + w; i < len; i += w) acc = f.fold(acc, x[i * stride]);
+      for (long long i = lane + w; i < len; i += w) acc = f.fold(acc, x[i * stride]);
+    }
     T reduced;
     if (w <= kWarp) {
       reduced = plane_tree(acc, w, f);
@@ -1331,6 +1356,17 @@ __global__ void __launch_bounds__(BS)
                          Fold{});
 }
 
+// PLANE on a compact plan (the combine over thousands of partials): the plane
+// body with the UnitPlan decode and the fold fixed at compile time. The general
+// kernel's by-value eight-dim geometry takes a private segment, which every
+// dispatch pays for (C4's combine: 12-14 us there).
+template <typename T, typename Fold>
+__global__ void __launch_bounds__(512)
+    reduce_plane_lean_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len) {
+  __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(T)];
+  plane_body<Fold, T>(out, in, up, static_cast<long long>(output_len), Fold{}, warp_lds);
+}
+
 // UNIT with the planner's blocks of BS threads.
 template <typename T, int BS>
 __global__ void __launch_bounds__(BS)
@@ -1630,6 +1666,40 @@ void launch_unit_lean(int op, unsigned threads, dim3 grid, dim3 block, hipStream
   }
 }
 
+// The lean plane kernel for `op` over the reference's op matrix for T.
+template <typename T>
+void launch_plane_lean(int op, dim3 grid, dim3 block, hipStream_t s, void* out, const void* in,
+                       const t4a::UnitPlan& up, unsigned int output_len) {
+  constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
+  constexpr bool kOrdered = kFloat || std::is_same_v<T, int> || std::is_same_v<T, long long>;
+  switch (op) {
+    case T4A_CUDA_REDUCE_SUM:
+      hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::SumFold>), grid, block, 0, s,
+                         out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_PROD:
+      hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::ProdFold>), grid, block, 0, s,
+                         out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_SUM_SQUARES:
+      if constexpr (kFloat)
+        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::SumSquaresFold>), grid, block,
+                           0, s, out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_MAX:
+      if constexpr (kOrdered)
+        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::MaxFold>), grid, block, 0, s,
+                           out, in, up, output_len);
+      break;
+    case T4A_CUDA_REDUCE_MIN:
+      if constexpr (kOrdered)
+        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::MinFold>), grid, block, 0, s,
+                           out, in, up, output_len);
+      break;
+    default: break;
+  }
+}
+
 }  // namespace
 
 extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int strategy,
@@ -1654,6 +1724,11 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
       const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, aligned);
       launch_unit_lean<T>(op, threads, grid, block, static_cast<hipStream_t>(stream), out, in,
                           up, static_cast<unsigned int>(output_len));
+    } else if (strategy == T4A_CUDA_REDUCE_PLANE && t4a::unit_plan_fits(rd, output_len) &&
+               block.y == 1 && block.z == 1 && threads <= 512u) {
+      const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, false);
+      launch_plane_lean<T>(op, grid, block, static_cast<hipStream_t>(stream), out, in, up,
+                           static_cast<unsigned int>(output_len));
     } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
                threads == static_cast<unsigned>(t4a::kBlock)) {
       hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kBlock>), grid, block, 0,
