@@ -67,7 +67,8 @@ typedef enum {
   T4A_HIP_ERR_LAUNCH = 100,        /* the HIP runtime refused the launch */
   T4A_HIP_ERR_NULL_ARGUMENT = 101, /* a required pointer argument is NULL */
   T4A_HIP_ERR_NOT_FOUND = 102,     /* no such code object, or the library's path is unknown */
-  T4A_HIP_ERR_TOO_SMALL = 103      /* a caller's buffer cannot hold the result */
+  T4A_HIP_ERR_TOO_SMALL = 103,     /* a caller's buffer cannot hold the result */
+  T4A_HIP_ERR_SCRATCH_LIMIT = 104  /* the partials exceed T4A_HIP_SCRATCH_BYTES */
 } t4a_status;
 
 /* Reference RankVariant (src/lib.rs:800-838): FAST selects the by-value symbol. */
@@ -346,6 +347,24 @@ int t4a_hip_reduction(void* out, const void* in, void* partials, int dtype, int 
                       const t4a_cuda_layout* out_layout, const t4a_cuda_layout* in_layout,
                       int axis, long long output_len, const t4a_reduction_plan* plan,
                       void* stream);
+
+/* t4a_hip_reduction without a caller's partials workspace, allocating nothing.
+ * No counterpart in the reference (its caller always owns the workspace); it is
+ * for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc. A Split plan's partials
+ * live in a library-owned device array of T4A_HIP_SCRATCH_BYTES per GPU (held
+ * until the process ends; its address is looked up on a device's first call);
+ * a plan whose partials layout needs more returns T4A_HIP_ERR_SCRATCH_LIMIT
+ * before touching the device. A Direct plan needs no workspace. Pass 1 writes
+ * every partial the combine reads, so nothing need start at zero. Every call on
+ * one GPU shares that GPU's array: calls on the same stream are ordered, calls
+ * that overlap on one GPU (other streams, other host threads) race. Same
+ * outputs, bit for bit, as t4a_hip_reduction with a workspace of its own. */
+#define T4A_HIP_SCRATCH_BYTES (8u * 1024u * 1024u)
+int t4a_hip_reduction_scratch(void* out, const void* in, int dtype, int op,
+                              const t4a_cuda_layout* out_layout,
+                              const t4a_cuda_layout* in_layout, int axis, long long output_len,
+                              const t4a_reduction_plan* plan, void* stream);
 
 /* 1 if t4a_hip_reduction runs `plan` over an input at `in` as one launch, else
  * 0 (no reference counterpart: it tells a caller which kernels a profile will

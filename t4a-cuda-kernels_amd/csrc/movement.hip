@@ -1263,6 +1263,12 @@ int status_of_last_launch() {
   last_launch_error = static_cast<int>(e);
   return T4A_HIP_ERR_LAUNCH;
 }
+
+int status_of_hip(int error) {
+  if (error == static_cast<int>(hipSuccess)) return T4A_OK;
+  last_launch_error = error;
+  return T4A_HIP_ERR_LAUNCH;
+}
 }  // namespace t4a
 
 extern "C" int t4a_hip_last_error(void) { return last_launch_error; }

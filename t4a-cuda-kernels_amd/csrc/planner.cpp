@@ -705,6 +705,7 @@ const char* t4a_status_name(int status) {
   if (status == T4A_HIP_ERR_NULL_ARGUMENT) return "NullArgument";
   if (status == T4A_HIP_ERR_NOT_FOUND) return "NotFound";
   if (status == T4A_HIP_ERR_TOO_SMALL) return "TooSmall";
+  if (status == T4A_HIP_ERR_SCRATCH_LIMIT) return "ScratchLimit";
   return "Unknown";
 }
 

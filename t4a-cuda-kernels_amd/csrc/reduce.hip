@@ -20,6 +20,7 @@
 //     elements of one or more rows instead of 32 elements a row apart.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "device.h"
@@ -27,8 +28,10 @@
 #include "t4a/t4a.h"
 
 namespace t4a {
-// Launch status of the last kernel launch on this thread (movement.hip).
+// Launch status of the last kernel launch on this thread, and the status of a
+// HIP runtime call's error (both record it for t4a_hip_last_error; movement.hip).
 int status_of_last_launch();
+int status_of_hip(int error);
 
 namespace {
 
@@ -2064,6 +2067,70 @@ extern "C" int t4a_hip_reduction_joins(const void* in, int dtype, int op,
   return joined_applies(in, dtype, op, *out_layout, *in_layout, pl, axis, output_len, *plan, &j)
              ? 1
              : 0;
+}
+
+// ---- a whole planned reduction that allocates nothing -----------------------------
+//
+// The partials workspace of t4a_hip_reduction_scratch: one array per GPU,
+// loaded with this library's code and held until the process ends. In host
+// code `scratch` names a host-side stand-in, not the device array: its device
+// address comes from hipGetSymbolAddress, once per device, and only that
+// address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[T4A_HIP_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_address[kScratchDevices];  // per device; nullptr until first looked up
+
+// The current device's address of `scratch` (looked up on the device's first
+// call, with that device current).
+int scratch_of_current_device(void** address) {
+  int device = -1;
+  if (int st = t4a::status_of_hip(static_cast<int>(hipGetDevice(&device)))) return st;
+  if (device < 0 || device >= kScratchDevices) return T4A_HIP_ERR_NOT_FOUND;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void* p = nullptr;
+    if (int st = t4a::status_of_hip(
+            static_cast<int>(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))))
+      return st;
+    if (p == nullptr) return T4A_HIP_ERR_NOT_FOUND;
+    scratch_address[device] = p;
+  }
+  *address = scratch_address[device];
+  return T4A_OK;
+}
+
+}  // namespace
+
+extern "C" int t4a_hip_reduction_scratch(void* out, const void* in, int dtype, int op,
+                                         const t4a_cuda_layout* out_layout,
+                                         const t4a_cuda_layout* in_layout, int axis,
+                                         long long output_len, const t4a_reduction_plan* plan,
+                                         void* stream) {
+  if (plan == nullptr || out_layout == nullptr || in_layout == nullptr)
+    return T4A_HIP_ERR_NULL_ARGUMENT;
+  if (plan->kind == T4A_PLAN_DIRECT)  // one pass: no workspace
+    return t4a_hip_reduction(out, in, nullptr, dtype, op, out_layout, in_layout, axis,
+                             output_len, plan, stream);
+  // The partials' size is checked before the device is touched.
+  t4a_cuda_layout pl;
+  if (int st = t4a_reduction_partials_layout(in_layout, static_cast<unsigned>(axis),
+                                             plan->split.splits, &pl))
+    return st;
+  long long count = 0;
+  if (int st = t4a_layout_element_count(&pl, &count)) return st;
+  const long long esize = t4a::dtype_size(dtype);
+  if (esize == 0) return T4A_OK;  // unknown tag: no work, as t4a_hip_reduction
+  if (count > static_cast<long long>(T4A_HIP_SCRATCH_BYTES) / esize)
+    return T4A_HIP_ERR_SCRATCH_LIMIT;
+  if (launch_empty(&plan->pass1)) return T4A_OK;
+  void* partials = nullptr;
+  if (int st = scratch_of_current_device(&partials)) return st;
+  return t4a_hip_reduction(out, in, partials, dtype, op, out_layout, in_layout, axis,
+                           output_len, plan, stream);
 }
 
 // The general-rank twins on the caller's stream with a planned geometry (any

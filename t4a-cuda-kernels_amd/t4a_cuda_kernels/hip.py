@@ -225,6 +225,21 @@ def reduction(plan: ReductionPlan, out, inp, partials, dtype: DType, op: ReduceO
         byref(plan.to_c()), _stream(stream)))
 
 
+# Bytes of the library's per-GPU partials array (T4A_HIP_SCRATCH_BYTES).
+SCRATCH_BYTES = 8 * 1024 * 1024
+
+
+def reduction_scratch(plan: ReductionPlan, out, inp, dtype: DType, op: ReduceOp,
+                      out_layout: Layout, in_layout: Layout, axis: int, output_len: int,
+                      stream=None) -> None:
+    """`reduction` without a partials workspace, allocating nothing: a Split
+    plan's partials live in the library's per-GPU array of SCRATCH_BYTES
+    (ScratchLimit when they do not fit). Calls that overlap on one GPU race."""
+    _check(_lib.load().t4a_hip_reduction_scratch(
+        _ptr(out), _ptr(inp), int(dtype), int(op), byref(out_layout.c), byref(in_layout.c), axis,
+        output_len, byref(plan.to_c()), _stream(stream)))
+
+
 def reduction_joins(plan: ReductionPlan, inp, dtype: DType, op: ReduceOp, out_layout: Layout,
                     in_layout: Layout, axis: int, output_len: int) -> bool:
     """Whether `reduction` runs `plan` over `inp` as one launch."""
