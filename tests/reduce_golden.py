@@ -21,6 +21,8 @@ from pathlib import Path
 
 import numpy as np
 
+from t4a_cuda_kernels import configs
+
 GOLDEN = Path(__file__).resolve().parent / "golden" / "reduce-golden.tsv"
 
 # (name, extents in reference axis-0-fastest order, axis)
@@ -39,24 +41,15 @@ DTYPES = {"F32": (0, 4, 1), "F64": (1, 8, 1), "C32": (5, 4, 2), "C64": (6, 8, 2)
 OPS = {"Sum": 0, "Prod": 1, "SumSquares": 2, "Max": 3, "Min": 4}
 CLASSES = ["Random", "NanPayloads", "Infs", "SignedZeros", "NegZeros", "Overflow"]
 
-_GAMMA = np.uint64(0x9E3779B97F4A7C15)
-_M1 = np.uint64(0xBF58476D1CE4E5B9)
-_M2 = np.uint64(0x94D049BB133111EB)
+# The config generator: SplitMix64 and unit() (t4a_cuda_kernels.configs). The
+# golden inputs are regenerated with it, so these vectors pin the generator the
+# benchmark and the config tests use.
+unit = configs.unit
 
 
 def splitmix_draws(seed: int, n: int) -> np.ndarray:
     """The first n outputs of SplitMix64(seed): state += gamma, then mix."""
-    k = np.arange(1, n + 1, dtype=np.uint64)
-    with np.errstate(over="ignore"):
-        z = np.uint64(seed) + k * _GAMMA
-        z = (z ^ (z >> np.uint64(30))) * _M1
-        z = (z ^ (z >> np.uint64(27))) * _M2
-    return z ^ (z >> np.uint64(31))
-
-
-def unit(draws: np.ndarray) -> np.ndarray:
-    """Uniform in [-1, 1) on a 2^-52 grid, exact in f64."""
-    return (draws >> np.uint64(11)).astype(np.float64) * (1.0 / float(1 << 52)) - 1.0
+    return configs.draws(seed, n)
 
 
 def fnv1a64_text(text: str) -> int:
