@@ -377,6 +377,12 @@ int t4a_hip_reduction_joins(const void* in, int dtype, int op, const t4a_cuda_la
  * T4A_HIP_ERR_LAUNCH (0 if none). */
 int t4a_hip_last_error(void);
 
+/* Kernel launches the t4a_hip_* launchers have issued in this process, all
+ * threads (no reference counterpart: the reference benchmark counts the
+ * launches in its measured region through its own launch wrapper,
+ * examples/bench_kernels.rs:283-306; this is that count for this library). */
+unsigned long long t4a_hip_launch_count(void);
+
 /* ---- code objects (the prepare step's artifacts) -------------------------- */
 
 /* The gfx950 code objects exporting the reference-named kernel entries, built

@@ -110,6 +110,13 @@ T4A_HD FastDiv fast_div(unsigned int d) {
   FastDiv f;
   if (d == 0) d = 1;  // no divisor of an empty walk is ever used; keep it defined
   f.d = d;
+  if (d > 0x80000000u) {
+    // Every dividend (x < 2^31) is below d: the quotient is 0, which m = 0 and
+    // a shift of 31 give exactly (the general form would shift by 32).
+    f.m = 0;
+    f.shift = 31;
+    return f;
+  }
   int l = 0;
   while ((1ull << l) < d) ++l;
   f.shift = l;
@@ -785,6 +792,20 @@ T4A_HD bool unit_plan_fits(const ReduceDims& rd, long long output_len) {
   return rd.n <= 3 && output_len < (1ll << 31) && rd.axis_len < (1ll << 31);
 }
 
+// A 32-bit grid-stride walk over `items` (index i < items, then i + S with
+// S = blocks * per_block) never wraps when items + S < 2^32. The lean kernels
+// walk their outputs or cubes that way, and any caller's grid reaches them, so
+// their launchers check it.
+T4A_HD bool grid_stride_fits(long long items, unsigned int blocks, unsigned long long per_block) {
+  if (items < 0) return false;
+  return static_cast<unsigned long long>(items) + per_block * blocks < (1ull << 32);
+}
+
+// The lean unit kernel's walk: a thread's outputs o0 + u * S (u <
+// kUnitOutputsPerThread, S = blocks * threads) and the next o0 +
+// kUnitOutputsPerThread * S.
+T4A_HD bool unit_lean_fits(long long output_len, unsigned int blocks, unsigned int threads);
+
 T4A_HD UnitPlan unit_plan(const ReduceDims& rd, int v, bool aligned) {
   UnitPlan up;
   up.in_offset = rd.in_offset;
@@ -810,6 +831,11 @@ T4A_HD UnitPlan unit_plan(const ReduceDims& rd, int v, bool aligned) {
 // multiple of V): a thread takes kUnitOutputsPerThread outputs at once, their
 // loads issued together.
 constexpr int kUnitOutputsPerThread = 4;
+
+T4A_HD bool unit_lean_fits(long long output_len, unsigned int blocks, unsigned int threads) {
+  return grid_stride_fits(output_len, blocks,
+                          static_cast<unsigned long long>(kUnitOutputsPerThread) * threads);
+}
 
 T4A_HD bool unit_one_group(const ReduceDims& rd, int dtype) {
   const int es = dtype_size(dtype);

@@ -11,6 +11,7 @@
 // grid-stride loops, so a block plans once and then streams tiles.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "device.h"
@@ -1254,10 +1255,13 @@ extern "C" __global__ void __launch_bounds__(256)
 
 namespace {
 thread_local int last_launch_error = 0;
+std::atomic<unsigned long long> launch_count{0};
 }  // namespace
 
 namespace t4a {
+// Called once right after every kernel launch of every t4a_hip_* launcher.
 int status_of_last_launch() {
+  launch_count.fetch_add(1, std::memory_order_relaxed);
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return T4A_OK;
   last_launch_error = static_cast<int>(e);
@@ -1273,11 +1277,22 @@ int status_of_hip(int error) {
 
 extern "C" int t4a_hip_last_error(void) { return last_launch_error; }
 
+extern "C" unsigned long long t4a_hip_launch_count(void) {
+  return launch_count.load(std::memory_order_relaxed);
+}
+
 namespace {
 using t4a::status_of_last_launch;
 
 bool launch_empty(const t4a_launch* l) {
   return l->grid[0] == 0 || l->grid[1] == 0 || l->grid[2] == 0;
+}
+
+// A block of exactly `threads` threads along x: the block-size-specialised
+// kernels number their threads by threadIdx.x alone (any other block shape
+// takes the kernels that read blockDim).
+bool one_dim(const dim3& block, int threads) {
+  return block.x == static_cast<unsigned>(threads) && block.y == 1 && block.z == 1;
 }
 
 
@@ -1396,7 +1411,7 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
       return status_of_last_launch();
     }
     if (plan.mode != t4a::kMoveTiled) {
-      if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+      if (one_dim(block, t4a::kBlock))
         hipLaunchKernelGGL((t4a::move_flat_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src,
                            plan);
       else
@@ -1459,8 +1474,7 @@ extern "C" int t4a_hip_tiled_transpose(void* dst, const void* src, int dtype,
     const long long tiles_m = (dst_fast_extent + TM - 1) / TM;
     const long long tiles_n = (src_fast_extent + TN - 1) / TN;
     t4a::TileOrder order{};
-    const bool planned =
-        block.x * block.y * block.z == static_cast<unsigned>(t4a::kTransposeBlock);
+    const bool planned = one_dim(block, t4a::kTransposeBlock);
     if (planned && grid.y == 1 && tiles_m > 0 && tiles_n > 0 &&
         tiles_m * tiles_n < (1ll << 30)) {
       order.tiles_m = t4a::fast_div(static_cast<unsigned int>(tiles_m));
@@ -1492,7 +1506,7 @@ extern "C" int t4a_hip_copy_exact(void* dst, const void* src, int dtype, long lo
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+    if (one_dim(block, t4a::kBlock))
       hipLaunchKernelGGL((t4a::copy_kernel<P, t4a::kBlock>), grid, block, 0, s, dst, src, len,
                          grid.x);
     else
@@ -1571,7 +1585,7 @@ extern "C" int t4a_hip_fill_zero(void* out, int dtype, long long len, const t4a_
   return with_payload(dtype, [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock))
+    if (one_dim(block, t4a::kBlock))
       hipLaunchKernelGGL((t4a::fill_kernel<P, t4a::kBlock>), grid, block, 0, s, out, len,
                          grid.x);
     else
@@ -1600,7 +1614,7 @@ extern "C" int t4a_hip_fill_zero_view(void* out, int dtype, const t4a_cuda_layou
     constexpr int V = t4a::tile_vector<P>();
     const bool vec =
         V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && t4a::fill_vectorizable(fp, V);
-    const bool planned = block.x * block.y * block.z == static_cast<unsigned>(t4a::kBlock);
+    const bool planned = one_dim(block, t4a::kBlock);
     if (vec && planned)
       hipLaunchKernelGGL((t4a::fill_view_kernel<P, V, t4a::kBlock>), grid, block, 0, s, out, fp,
                          grid.x);

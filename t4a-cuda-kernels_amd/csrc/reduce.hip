@@ -1720,9 +1720,12 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
   return with_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
     const unsigned threads = block.x * block.y * block.z;
-    if (strategy == T4A_CUDA_REDUCE_UNIT && t4a::unit_plan_fits(rd, output_len) &&
+    // The block-size-specialised kernels number threads by x alone.
+    const bool flat_blocks = block.y == 1 && block.z == 1;
+    if (strategy == T4A_CUDA_REDUCE_UNIT && t4a::unit_plan_fits(rd, output_len) && flat_blocks &&
         (threads == static_cast<unsigned>(t4a::kBlock) ||
-         threads == static_cast<unsigned>(t4a::kUnitSmallBlock))) {
+         threads == static_cast<unsigned>(t4a::kUnitSmallBlock)) &&
+        t4a::unit_lean_fits(output_len, grid.x, threads)) {
       const bool aligned = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
       const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, aligned);
       launch_unit_lean<T>(op, threads, grid, block, static_cast<hipStream_t>(stream), out, in,
@@ -1732,11 +1735,11 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
       const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, false);
       launch_plane_lean<T>(op, grid, block, static_cast<hipStream_t>(stream), out, in, up,
                            static_cast<unsigned int>(output_len));
-    } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
+    } else if (strategy == T4A_CUDA_REDUCE_UNIT && flat_blocks &&
                threads == static_cast<unsigned>(t4a::kBlock)) {
       hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kBlock>), grid, block, 0,
                          static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
-    } else if (strategy == T4A_CUDA_REDUCE_UNIT &&
+    } else if (strategy == T4A_CUDA_REDUCE_UNIT && flat_blocks &&
                threads == static_cast<unsigned>(t4a::kUnitSmallBlock)) {
       hipLaunchKernelGGL((t4a::reduce_unit_kernel<T, t4a::kUnitSmallBlock>), grid, block, 0,
                          static_cast<hipStream_t>(stream), out, in, op, rd, output_len);
@@ -1824,7 +1827,11 @@ extern "C" int t4a_hip_reduce_partials(void* partials, const void* in, int dtype
   const dim3 block(launch->block[0], launch->block[1], launch->block[2]);
   const bool sideways = pp.mode != t4a::kPartialsPlane;
   const bool aligned_in = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-  const int lean = !sideways && whole_waves && aligned_in
+  // The lean mapping walks cubes with 32-bit indices, a grid stride of eight
+  // planes per block.
+  const int lean = !sideways && whole_waves && aligned_in &&
+                           t4a::grid_stride_fits(pp.units, launch->grid[0],
+                                                 t4a::kBlock / t4a::kWarp)
                        ? t4a::lean_slots(pp, dtype, op, splits, chunk_len, w)
                        : 0;
   const bool stream_mode = !lean && !sideways && whole_waves && aligned_in &&

@@ -224,6 +224,7 @@ SIGNATURES = {
     "t4a_hip_reduction": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int,
                                   POINTER(CLayout), POINTER(CLayout), c_int, c_longlong,
                                   POINTER(CReductionPlan), c_void_p]),
+    "t4a_hip_launch_count": (ctypes.c_ulonglong, []),
     "t4a_hip_reduction_scratch": (c_int, [c_void_p, c_void_p, c_int, c_int, POINTER(CLayout),
                                           POINTER(CLayout), c_int, c_longlong,
                                           POINTER(CReductionPlan), c_void_p]),

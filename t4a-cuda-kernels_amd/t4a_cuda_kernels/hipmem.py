@@ -19,6 +19,20 @@ from . import _lib
 H2D, D2H, D2D = 1, 2, 3
 _HIP = None
 
+# What this process has asked of the device through this module: device
+# allocations, bytes copied (either direction, device to device included),
+# memsets, host waits (device, stream and event synchronizations) and module
+# kernel launches. A benchmark snapshots them around its timed region, as the
+# reference benchmark does with its own counters (examples/bench_kernels.rs:
+# 86-152); kernel launches of the library itself are t4a_hip_launch_count().
+COUNTS = {"allocations": 0, "transfer_bytes": 0, "fills": 0, "host_waits": 0,
+          "module_launches": 0}
+
+
+def counts() -> dict:
+    """A copy of COUNTS."""
+    return dict(COUNTS)
+
 
 def hip() -> ctypes.CDLL:
     """The HIP runtime already mapped by libt4a_hip.so (same soname, same handle)."""
@@ -84,6 +98,7 @@ def device_name(device: int = 0) -> str:
 
 
 def synchronize() -> None:
+    COUNTS["host_waits"] += 1
     check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
 
 
@@ -93,6 +108,7 @@ class DeviceBuffer:
     def __init__(self, nbytes: int):
         self.nbytes = int(nbytes)
         p = c_void_p()
+        COUNTS["allocations"] += 1
         check(hip().hipMalloc(byref(p), max(self.nbytes, 1)), f"hipMalloc({self.nbytes})")
         self.ptr = p.value
 
@@ -111,23 +127,29 @@ class DeviceBuffer:
     def upload(self, arr: np.ndarray, offset: int = 0) -> None:
         arr = np.ascontiguousarray(arr)
         assert offset + arr.nbytes <= self.nbytes
+        COUNTS["transfer_bytes"] += arr.nbytes
         if arr.nbytes:
             check(hip().hipMemcpy(c_void_p(self.ptr + offset), c_void_p(arr.ctypes.data),
                                   arr.nbytes, H2D), "hipMemcpy H2D")
 
-    def download(self, nbytes: int | None = None) -> np.ndarray:
-        n = self.nbytes if nbytes is None else int(nbytes)
+    def download(self, nbytes: int | None = None, offset: int = 0) -> np.ndarray:
+        """`nbytes` (default: the rest of the buffer) from byte `offset`."""
+        n = self.nbytes - offset if nbytes is None else int(nbytes)
+        assert 0 <= offset and offset + n <= self.nbytes
         out = np.empty(n, dtype=np.uint8)
+        COUNTS["transfer_bytes"] += n
         if n:
-            check(hip().hipMemcpy(c_void_p(out.ctypes.data), c_void_p(self.ptr), n, D2H),
-                  "hipMemcpy D2H")
+            check(hip().hipMemcpy(c_void_p(out.ctypes.data), c_void_p(self.ptr + offset), n,
+                                  D2H), "hipMemcpy D2H")
         return out
 
     def copy_from(self, other: "DeviceBuffer") -> None:
         n = min(self.nbytes, other.nbytes)
+        COUNTS["transfer_bytes"] += n
         check(hip().hipMemcpy(c_void_p(self.ptr), c_void_p(other.ptr), n, D2D), "hipMemcpy D2D")
 
     def fill(self, byte: int) -> None:
+        COUNTS["fills"] += 1
         check(hip().hipMemset(c_void_p(self.ptr), int(byte), self.nbytes), "hipMemset")
 
     def free(self) -> None:
@@ -155,6 +177,7 @@ class Stream:
         return self.handle or 0
 
     def synchronize(self) -> None:
+        COUNTS["host_waits"] += 1
         check(hip().hipStreamSynchronize(c_void_p(self.handle)), "hipStreamSynchronize")
 
     def __del__(self):
@@ -220,6 +243,7 @@ class Event:
         check(hip().hipEventRecord(c_void_p(self.handle), s), "hipEventRecord")
 
     def synchronize(self) -> None:
+        COUNTS["host_waits"] += 1
         check(hip().hipEventSynchronize(c_void_p(self.handle)), "hipEventSynchronize")
 
     def elapsed_ms(self, end: "Event") -> float:
@@ -261,11 +285,32 @@ class Module:
         `args` (by-value structs included); an empty grid launches nothing."""
         if 0 in tuple(grid):
             return
+        COUNTS["module_launches"] += 1
         params = (c_void_p * len(args))(*[ctypes.cast(byref(a), c_void_p) for a in args])
         s = c_void_p(stream.handle if isinstance(stream, Stream) else (stream or 0))
         check(hip().hipModuleLaunchKernel(c_void_p(self.function(name)), *map(int, grid),
                                           *map(int, block), int(shared_bytes), s, params, None),
               f"hipModuleLaunchKernel({name})")
+
+    def bind(self, name: str, grid, block, shared_bytes: int, stream, args):
+        """`launch` with the argument block built once: returns a callable that
+        launches `name` again with the same arguments (their ctypes objects are
+        kept alive by the callable)."""
+        if 0 in tuple(grid):
+            return lambda: None
+        params = (c_void_p * len(args))(*[ctypes.cast(byref(a), c_void_p) for a in args])
+        s = c_void_p(stream.handle if isinstance(stream, Stream) else (stream or 0))
+        fn = c_void_p(self.function(name))
+        g, b = tuple(map(int, grid)), tuple(map(int, block))
+        lib = hip()
+        keep = (params, args)
+
+        def go():
+            COUNTS["module_launches"] += 1
+            check(lib.hipModuleLaunchKernel(fn, *g, *b, int(shared_bytes), s, params, None),
+                  f"hipModuleLaunchKernel({name})")
+        go.keep = keep
+        return go
 
     def unload(self) -> None:
         if getattr(self, "handle", None):

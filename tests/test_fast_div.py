@@ -1,8 +1,8 @@
 """The kernels' multiply-shift division (FastDiv in csrc/geometry.h), CPU only:
 compiled with g++ from the same header and checked against exact division for
-every divisor up to 5000 and random ones up to 2^31 - 1, at dividends that
-cover each divisor's multiples and their neighbours, small values and values
-just below the 2^31 bound."""
+every divisor up to 5000, random ones up to 2^31 - 1 and divisors from 2^31 - 2
+to 2^32 - 1, at dividends that cover each divisor's multiples and their
+neighbours, small values and values just below the 2^31 bound."""
 import subprocess
 from pathlib import Path
 
@@ -35,6 +35,13 @@ int main() {
     for (unsigned x = top - 64; x < top; ++x) if (!check(d, x)) return 1;
     if (!check(d, top)) return 1;
   }
+  // Divisors from 2^31 up: every dividend below 2^31 has quotient 0 (2^31
+  // itself takes the general form, larger ones the special one).
+  for (unsigned long long d = 0x7ffffffeull; d <= 0xffffffffull; d += (d < 0x80000010ull ? 1 : 0x0fffffffull)) {
+    for (unsigned x : {0u, 1u, 2u, 12345u, top - 1, top}) if (!check((unsigned)d, x)) return 1;
+    for (int k = 0; k < 64; ++k) if (!check((unsigned)d, (unsigned)(rng() % ((unsigned long long)top + 1)))) return 1;
+  }
+  if (!check(0xffffffffu, top) || !check(0x80000001u, top)) return 1;
   for (int i = 0; i < 200000; ++i) {
     const unsigned d = 1 + (unsigned)(rng() % top);
     const unsigned x = (unsigned)(rng() % ((unsigned long long)top + 1));

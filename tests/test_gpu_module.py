@@ -255,6 +255,44 @@ def test_module_reduce(modules, dtype):
 
 
 @pytest.mark.parametrize("dtype", REAL, ids=[d.name for d in REAL])
+def test_module_wide_plane_boundaries(modules, dtype):
+    """The entry's wide plane folds (widths 64-512) at axis lengths on both sides
+    of the plane body's switch from up-front loads (16 * width) to the serial
+    walk (16 * width + 1, about 40 * width), under both geometries."""
+    rng = np.random.default_rng(36)
+    for width in (64, 128, 256, 512):
+        for extents, axis in [([16 * width, 2], 0), ([16 * width + 1, 2], 0),
+                              ([40 * width + 3, 1], 0), ([3, 16 * width + 1], 1)]:
+            n = int(np.prod(extents))
+            x = reduce_inputs(dtype, n, rng)
+            d_in = to_device(x)
+            in_l = t.Layout.compact(extents)
+            oe = list(extents)
+            oe[axis] = 1
+            out_l = t.Layout.compact(oe)
+            on = out_l.element_count()
+            for op in (t.ReduceOp.Sum, t.ReduceOp.Max):
+                if not supported(dtype, op):
+                    continue
+                plan = t.plan_reduce(dtype, op, t.ReduceStrategy.Plane, out_l, on, in_l, n, axis,
+                                     width)
+                want = np.zeros(on, dtype=NUMPY[dtype])
+                orc.reduce(want, x, dtype, op, t.ReduceStrategy.Plane, width, out_l, in_l, axis,
+                           on)
+                for who, geo in (("reference", ref_reduce(t.ReduceStrategy.Plane, on, width)),
+                                 ("ours", ours(plan))):
+                    say("module wide plane", dtype.name, op.name, extents, axis, width, who, geo)
+                    d_out = sentinel(want.nbytes)
+                    modules["reduce"].launch(
+                        "t4a_cuda_reduce", *geo, None,
+                        [ptr(d_out), ptr(d_in), c_int(dtype), c_int(op),
+                         c_int(t.ReduceStrategy.Plane), out_l.c, in_l.c, c_int(axis), c_ll(on)])
+                    got = to_host(d_out, want.nbytes)
+                    assert np.array_equal(got, want.view(np.uint8)), (extents, axis, op, width,
+                                                                      who)
+
+
+@pytest.mark.parametrize("dtype", REAL, ids=[d.name for d in REAL])
 def test_module_reduce_partials(modules, dtype):
     rng = np.random.default_rng(35)
     shapes = [([3, 5000], 1), ([40000], 0), ([2600, 3], 0), ([64, 3000], 1)]

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import t4a_cuda_kernels as t
-from t4a_cuda_kernels import hip
+from t4a_cuda_kernels import configs, hip
 from gpu_util import (NUMPY, SENTINEL, random_elements, say, sentinel, stream, to_device,
                       to_host)
 from oracle import t4a_oracle as orc
@@ -34,10 +34,10 @@ def c_order_permute_view(c_shape, perm, dtype_size=None):
     return ext, st
 
 
-def run_transpose(dtype, m, n, batches, offset, rng):
+def run_transpose(dtype, m, n, batches, offset, rng, src=None):
     es = dtype.size
     src_len = offset + m * n * batches
-    src = random_elements(dtype, src_len, rng)
+    src = random_elements(dtype, src_len, rng) if src is None else src
     dst_len = m * n * batches
     say("transpose", dtype.name, m, n, batches, offset)
     plan = t.plan_tiled_transpose(dtype, t.TransposeConfig.DEFAULT, offset, m * n, m, n,
@@ -144,10 +144,10 @@ def test_copy_exact_full_size():
     assert np.array_equal(to_host(d_dst, count * 4), src.view(np.uint8))
 
 
-def run_materialize(dtype, layout, rng, src_len=None):
+def run_materialize(dtype, layout, rng, src_len=None, src=None):
     count = layout.element_count()
     src_len = src_len if src_len is not None else max(layout.max_reachable_offset() + 1, 1)
-    src = random_elements(dtype, src_len, rng)
+    src = random_elements(dtype, src_len, rng) if src is None else src
     say("materialize", dtype.name, layout)
     plan = t.plan_materialize_strided(dtype, layout, src_len)
     d_src = to_device(src)
@@ -159,11 +159,11 @@ def run_materialize(dtype, layout, rng, src_len=None):
     assert np.array_equal(got, want.view(np.uint8)), f"materialize {dtype.name} {layout}"
 
 
-def run_strided(dtype, src_layout, dst_layout, rng, dst_len=None):
+def run_strided(dtype, src_layout, dst_layout, rng, dst_len=None, src=None):
     count = src_layout.element_count()
     src_len = max(src_layout.max_reachable_offset() + 1, 1)
     dst_len = dst_len if dst_len is not None else max(dst_layout.max_reachable_offset() + 1, 1)
-    src = random_elements(dtype, src_len, rng)
+    src = random_elements(dtype, src_len, rng) if src is None else src
     say("strided_to_strided", dtype.name, src_layout, dst_layout)
     plan = t.plan_strided_to_strided(dtype, src_layout, src_len, dst_layout, dst_len)
     d_src = to_device(src)
@@ -224,21 +224,30 @@ def test_strided_to_strided_random_views(dtype):
         run_strided(dtype, src, t.Layout(ext, st, int(rng.integers(0, 7))), rng)
 
 
+def test_config_c1_transpose_and_its_8192_twin():
+    """C1: f32 C-[1024, 1024] transposed (1,0), and the 8192^2 roofline twin, on
+    the configuration's seeded inputs (t4a_cuda_kernels.configs)."""
+    for m in (1024, 8192):
+        run_transpose(t.DType.F32, m, m, 1, 0, None, src=configs.c1_input(m))
+
+
 def test_config_c3_reversed_rank4_permute_f64_and_c32():
-    """C3: C-shape [64,128,64,32], permutation (3,1,0,2), source axis 1 reversed."""
-    rng = np.random.default_rng(2)
+    """C3: C-shape [64,128,64,32], permutation (3,1,0,2), source axis 1 reversed,
+    on the configuration's seeded N(0,1) inputs."""
     src_l = t.Layout([64, 64, 128, 32], [32, 262144, -2048, 1], 260096)
     dst_l = t.Layout.compact([64, 64, 128, 32])
-    for dtype in (t.DType.F64, t.DType.C32):
-        run_strided(dtype, src_l, dst_l, rng)
-        run_materialize(dtype, src_l, rng)
+    assert src_l.max_reachable_offset() + 1 == 1 << 24
+    for dtype, npt in ((t.DType.F64, np.float64), (t.DType.C32, np.complex64)):
+        x = configs.c3_input(npt)
+        run_strided(dtype, src_l, dst_l, None, src=x)
+        run_materialize(dtype, src_l, None, src=x)
 
 
 def test_config_c5_rank6_c64_permute():
     """C5: c64 C-shape [16]^6 permuted by (5,2,0,4,1,3) into a compact output."""
     ext, st = c_order_permute_view([16] * 6, (5, 2, 0, 4, 1, 3))
     assert st == [256, 65536, 16, 1048576, 4096, 1]
-    rng = np.random.default_rng(4)
     src_l = t.Layout(ext, st, 0)
-    run_materialize(t.DType.C64, src_l, rng)
-    run_strided(t.DType.C64, src_l, t.Layout.compact(ext), rng)
+    x = configs.c5_input()
+    run_materialize(t.DType.C64, src_l, None, src=x)
+    run_strided(t.DType.C64, src_l, t.Layout.compact(ext), None, src=x)

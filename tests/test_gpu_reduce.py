@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 import t4a_cuda_kernels as t
-from t4a_cuda_kernels import hip
+from t4a_cuda_kernels import configs, hip
 from gpu_util import NUMPY, say, sentinel, stream, to_device, to_host
 from oracle import t4a_oracle as orc
 
@@ -120,17 +120,31 @@ def run(dtype, op, in_l, axis, out_l, width, data, *, plan=None, explicit=None):
     else:
         pl = t.reduction_partials_layout(in_l, axis, plan.split.splits)
         pn = pl.element_count()
-        d_part = sentinel(pn * es)
-        hip.enqueue_reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, axis, on,
-                              stream())
         want_part = np.zeros(pn, dtype=NUMPY[dtype])
         orc.reduce_partials(want_part, data, dtype, op, width, pl, in_l, axis, on,
                             plan.split.splits, plan.split.chunk_len)
-        got_part = to_host(d_part, pn * es, "partials")
-        assert _nan_equal(dtype, got_part, want_part.view(np.uint8)), "pass-1 partials differ"
         bw = plan.pass2.block[0] if plan.combine_strategy == t.ReduceStrategy.Plane else width
         orc.reduce(want_out, want_part, dtype, plan.combine_op, plan.combine_strategy, bw,
                    out_l, pl, axis, on)
+        # Both doors of a split plan: the caller's two launches, and the whole
+        # plan through t4a_hip_reduction (one joined launch where it joins).
+        joins = hip.reduction_joins(plan, d_in, dtype, op, out_l, in_l, axis, on)
+        for door in ("two launches", "t4a_hip_reduction"):
+            say("  door:", door, "(joined)" if door != "two launches" and joins else "")
+            d_part = sentinel(pn * es)
+            d_out = sentinel(out_len * es)
+            if door == "two launches":
+                hip.enqueue_reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, axis,
+                                      on, stream())
+            else:
+                hip.reduction(plan, d_out, d_in, d_part, dtype, op, out_l, in_l, axis, on,
+                              stream())
+            got_part = to_host(d_part, pn * es, "partials")
+            assert _nan_equal(dtype, got_part, want_part.view(np.uint8)), \
+                f"pass-1 partials differ ({door})"
+            got = to_host(d_out, out_len * es, "output")
+            assert _nan_equal(dtype, got, want_out.view(np.uint8)), f"finals differ ({door})"
+        return plan, got.view(NUMPY[dtype])
     got = to_host(d_out, out_len * es, "output")
     assert _nan_equal(dtype, got, want_out.view(np.uint8)), "finals differ"
     return plan, got.view(NUMPY[dtype])
@@ -161,11 +175,18 @@ def test_direct_unit_and_plane(dtype, op):
 
 @pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
 def test_wide_plane_widths(dtype, op):
+    """Widths 64-512, with axis lengths on both sides of the plane body's switch
+    from loads issued up front (a lane walks at most 16 elements: length 16 *
+    width) to the serial walk joined across wavefronts through LDS (16 * width +
+    1, about 40 * width), on a contiguous and on a strided axis."""
     rng = np.random.default_rng(200 + 10 * int(dtype) + int(op))
     for bw in (64, 128, 256, 512):
-        compact_case(dtype, op, (3, bw * 5 + 7), 1, 32, rng,
-                     explicit=(t.ReduceStrategy.Plane, bw))
-        compact_case(dtype, op, (bw + 1, 2), 0, 32, rng, explicit=(t.ReduceStrategy.Plane, bw))
+        plane = (t.ReduceStrategy.Plane, bw)
+        compact_case(dtype, op, (3, bw * 5 + 7), 1, 32, rng, explicit=plane)
+        compact_case(dtype, op, (bw + 1, 2), 0, 32, rng, explicit=plane)
+        for length in (16 * bw, 16 * bw + 1, 40 * bw + 3):
+            compact_case(dtype, op, (2, length), 1, 32, rng, explicit=plane)
+        compact_case(dtype, op, (16 * bw + 1, 3), 0, 32, rng, explicit=plane)
 
 
 @pytest.mark.parametrize("dtype,op", PAIRS, ids=[f"{d.name}-{o.name}" for d, o in PAIRS])
@@ -350,29 +371,34 @@ def test_empty_output_is_no_launch():
 
 # ---- configuration shapes -----------------------------------------------------------
 
+# Inputs are the configurations' own (t4a_cuda_kernels.configs: SplitMix64 of the
+# config's seed), the ones bench.py times. Every split plan runs through both
+# doors (see run()): C2's inner-axis f32 Sum and Max through t4a_hip_reduction
+# are the joined kernel over all 8192 outputs.
+
 def test_config_c2_f32_inner_and_outer_sum_max_and_i64_sum():
-    rng = np.random.default_rng(1)
-    x = rng.uniform(-1.0, 1.0, 8192 * 8192).astype(np.float32)
+    x, xi = configs.c2_inputs()
     in_l = t.Layout.compact([8192, 8192])
     for axis, out_ext in ((0, [1, 8192]), (1, [8192, 1])):
+        out_l = t.Layout.compact(out_ext)
         for op in (Sum, Max):
-            plan, finals = run(F32, op, in_l, axis, t.Layout.compact(out_ext), 32, x)
+            plan = t.plan_reduction(F32, op, out_l, 8192, in_l, x.size, axis, 32)
+            assert hip.reduction_joins(plan, 1 << 20, F32, op, out_l, in_l, axis, 8192) == \
+                (axis == 0), (axis, op)
+            plan, finals = run(F32, op, in_l, axis, out_l, 32, x)
             assert plan.kind == "Split" and plan.split.splits == 32
-            check_f64_reference(F32, op, x, in_l, axis, t.Layout.compact(out_ext), finals)
-    xi = rng.integers(-1000, 1001, 8192 * 8192).astype(np.int64)
+            check_f64_reference(F32, op, x, in_l, axis, out_l, finals)
     run(I64, Sum, in_l, 0, t.Layout.compact([1, 8192]), 32, xi)
 
 
 def test_config_c4_middle_axis_and_i32_product():
-    rng = np.random.default_rng(3)
     ext = [4, 1048576, 32]  # C-shape [32, 1048576, 4]
     in_l = t.Layout.compact(ext)
-    x = rng.standard_normal(in_l.element_count()).astype(np.float32)
+    x, xi = configs.c4_inputs()
     for op in (SumSq, Min):
         plan, finals = run(F32, op, in_l, 1, t.Layout.compact([4, 1, 32]), 32, x)
         assert plan.split.splits == 4096
         check_f64_reference(F32, op, x, in_l, 1, t.Layout.compact([4, 1, 32]), finals)
-    xi = rng.choice(np.array([-1, 1, 2], dtype=np.int32), in_l.element_count())
     plan, _ = run(I32, Prod, in_l, 0, t.Layout.compact([1, 1048576, 32]), 32, xi)
     assert plan.kind == "Direct" and plan.strategy == t.ReduceStrategy.Unit
 
@@ -380,10 +406,9 @@ def test_config_c4_middle_axis_and_i32_product():
 def test_config_c5_sum_over_permuted_axis():
     """Sum over C-axis 3 of the (5,2,0,4,1,3)-permuted c64 [16]^6 tensor (stored
     compact after the permute): reference axis 2, stride 256, length 16."""
-    rng = np.random.default_rng(4)
     ext = [16] * 6
     in_l = t.Layout.compact(ext)
-    x = (rng.standard_normal(16**6) + 1j * rng.standard_normal(16**6)).astype(np.complex128)
+    x = configs.c5_input()
     out_ext = list(ext)
     out_ext[2] = 1
     out_l = t.Layout.compact(out_ext)
