@@ -33,6 +33,31 @@ __device__ __forceinline__ int block_threads() {
   }
 }
 
+// The reference-named entries plan inside the kernel: thread 0 of each block
+// derives the plan from the entry's arguments before the block's first load.
+// Under the reference planner's geometry -- a thread per element or per
+// output, 65,536 blocks for a 16M-element move -- that planning would run once
+// per block, round after round of resident blocks. So an entry keeps at most
+// kEntryWaves wavefronts' worth of blocks of the grid's first row working
+// (blocks past that, and blocks off the first row, return before planning),
+// and the kept blocks walk all of the work with their own count as the grid
+// stride. 2048 wavefronts (512 blocks of 256 threads) fill about half of what
+// the entries' registers and LDS let the chip hold, so the returning blocks
+// pass through the remaining slots while the working ones stream; a cap at
+// full residency would hold them back until the work is done.
+constexpr unsigned int kEntryWaves = 2048;
+
+__device__ __forceinline__ unsigned int entry_blocks() {
+  const unsigned int waves_per_block = (blockDim.x * blockDim.y * blockDim.z + 63u) / 64u;
+  unsigned int cap = kEntryWaves / (waves_per_block ? waves_per_block : 1u);
+  if (cap == 0) cap = 1;
+  return gridDim.x < cap ? gridDim.x : cap;
+}
+
+__device__ __forceinline__ bool entry_block_idle() {
+  return blockIdx.y != 0 || blockIdx.z != 0 || blockIdx.x >= entry_blocks();
+}
+
 using c32 = t4a_cuda_c32;
 using c64 = t4a_cuda_c64;
 

@@ -212,7 +212,7 @@ __device__ __forceinline__ bool transpose_config_valid(const t4a_cuda_transpose_
 // TILED: an la x lb tile; element (i, j) sits at src_base + src_a[i] + j and at
 // dst_base + i + dst_b[j]. VL / VS: elements per load / store.
 //
-// A block walks tiles t, t + gridDim.x, ... and keeps a tile's loads in flight
+// A block walks tiles t, t + blocks, ... and keeps a tile's loads in flight
 // while it writes the previous one: it loads tile t into registers, parks them
 // in LDS, then issues tile t+1's loads before reading tile t back out of LDS
 // and storing it. Tile coordinates are A-tile fastest, then B-tile, then the
@@ -284,10 +284,15 @@ constexpr int max_tile_elems() {
   return sizeof(P) >= 16 ? 32 * 32 : sizeof(P) >= 8 ? 64 * 32 : 64 * 64;
 }
 
-template <typename P, int VL, int VS>
+// `Pipelined`: with kTileThreads threads a block holds the next tile's loads in
+// registers while it stores the current one (the launchers' kernel); the
+// entries, which carry every plan's code in one kernel, take the one-tile-at-a-
+// time walk, whose registers do not cap the occupancy of all their paths.
+template <typename P, int VL, int VS, bool Pipelined>
 __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restrict__ src,
                                            const MovePlan& p, const long long* src_a,
-                                           const long long* dst_b, P* tile) {
+                                           const long long* dst_b, P* tile,
+                                           unsigned int blocks) {
   const int la = static_cast<int>(p.la);
   const int lb = static_cast<int>(p.lb);
   const int pitch = lb + 1;
@@ -308,9 +313,9 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
     }
   };
   long long t = blockIdx.x;
-  if (blockDim.x != kTileThreads) {
+  if (!Pipelined || blockDim.x != kTileThreads) {
     // Any other block size: load, park, store, one tile at a time.
-    for (; t < p.tiles; t += gridDim.x) {
+    for (; t < p.tiles; t += blocks) {
       const TileCoords tc = tile_coords(p, t);
       const P* s = src + tc.sbase;
       for (int e = tid; e < la * lbv; e += blockDim.x) {
@@ -358,7 +363,7 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
       }
     }
     __syncthreads();
-    const long long next = t + gridDim.x;
+    const long long next = t + blocks;
     TileCoords nxt = cur;
     if (next < p.tiles) {
       nxt = tile_coords(p, next);
@@ -526,40 +531,42 @@ __device__ __forceinline__ void tile_tables(const MovePlan& p, unsigned char* ld
   __syncthreads();
 }
 
-template <typename P, int VL, int VS>
+template <typename P, int VL, int VS, bool Pipelined>
 __device__ __forceinline__ void move_tiled_as(void* dst, const void* src, const MovePlan& p,
-                                              unsigned char* lds) {
+                                              unsigned char* lds, unsigned int blocks) {
   tile_tables(p, lds);
   const long long* src_a = reinterpret_cast<const long long*>(lds);
-  move_tiles<P, VL, VS>(static_cast<P*>(dst), static_cast<const P*>(src), p, src_a,
+  move_tiles<P, VL, VS, Pipelined>(static_cast<P*>(dst), static_cast<const P*>(src), p, src_a,
                         src_a + kMoveRunMax,
-                        reinterpret_cast<P*>(lds + 2 * kMoveRunMax * sizeof(long long)));
+                        reinterpret_cast<P*>(lds + 2 * kMoveRunMax * sizeof(long long)), blocks);
 }
 
+// The entries' tiled walk (one tile at a time).
 template <typename P>
 __device__ __forceinline__ void move_tiled(void* dst, const void* src, const MovePlan& p,
-                                           unsigned char* lds) {
+                                           unsigned char* lds, unsigned int blocks) {
   constexpr int V = tile_vector<P>();
   bool vl, vs;
   tile_vectorizable(p, V, dst, src, &vl, &vs);
   if (vl && vs) {
-    move_tiled_as<P, V, V>(dst, src, p, lds);
+    move_tiled_as<P, V, V, false>(dst, src, p, lds, blocks);
   } else if (vl) {
-    move_tiled_as<P, V, 1>(dst, src, p, lds);
+    move_tiled_as<P, V, 1, false>(dst, src, p, lds, blocks);
   } else if (vs) {
-    move_tiled_as<P, 1, V>(dst, src, p, lds);
+    move_tiled_as<P, 1, V, false>(dst, src, p, lds, blocks);
   } else {
-    move_tiled_as<P, 1, 1>(dst, src, p, lds);
+    move_tiled_as<P, 1, 1, false>(dst, src, p, lds, blocks);
   }
 }
 
 // CONTIG: rows along the fused dim `row_dim`, contiguous on both sides.
 template <typename P, int BS>
-__device__ __forceinline__ void move_rows(void* dst, const void* src, const MovePlan& p) {
+__device__ __forceinline__ void move_rows(void* dst, const void* src, const MovePlan& p,
+                                          unsigned int blocks) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
   const int bs = block_threads<BS>();
-  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  const long long gstride = static_cast<long long>(blocks) * bs;
   for (long long f = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; f < p.len;
        f += gstride) {
     long long rest = f / p.row_len;
@@ -615,11 +622,12 @@ __device__ __forceinline__ void move_row_units(void* dst, const void* src, const
 
 // GENERIC: one decode per element on both sides.
 template <typename P, int BS>
-__device__ __forceinline__ void move_elements(void* dst, const void* src, const MovePlan& p) {
+__device__ __forceinline__ void move_elements(void* dst, const void* src, const MovePlan& p,
+                                              unsigned int blocks) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
   const int bs = block_threads<BS>();
-  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  const long long gstride = static_cast<long long>(blocks) * bs;
   for (long long f = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; f < p.len;
        f += gstride) {
     long long rest = f;
@@ -652,12 +660,12 @@ __device__ __forceinline__ T uniform_copy(const T& shared_value) {
 
 // TILED inside the entries: when the plan has a one-tile shape (tile_plan),
 // thread 0 writes the TilePlan into the block's move scratch behind the tile,
-// and the block moves tiles blockIdx.x, blockIdx.x + gridDim.x, ... with the
+// and the block moves tiles blockIdx.x, blockIdx.x + blocks, ... with the
 // launchers' one-tile body, so a persistent grid plans once per block; other
-// plans and block sizes take the pipelined tile walk.
+// plans and block sizes take the general tile walk, one tile at a time.
 template <typename P>
 __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, const MovePlan& p,
-                                                 unsigned char* lds) {
+                                                 unsigned char* lds, unsigned int blocks) {
   if constexpr (sizeof(P) >= 4) {
     constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
     constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
@@ -675,11 +683,14 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
         tile_vectorizable(p, V, dst, src, &vl, &vs);
         P* tile = reinterpret_cast<P*>(lds);
         const unsigned int tiles = static_cast<unsigned int>(p.tiles);
-        const TilePlan tp = uniform_copy(*shared_tp);
+        // Read from LDS: copied to scalar registers, the plan overflows the
+        // scalar file, and the spills into vector registers halve the
+        // occupancy of every path of the entry kernel.
+        const TilePlan& tp = *shared_tp;
         auto walk = [&](auto vl_tag, auto vs_tag) {
           constexpr int VLt = decltype(vl_tag)::value;
           constexpr int VSt = decltype(vs_tag)::value;
-          for (unsigned int t = blockIdx.x; t < tiles; t += gridDim.x) {
+          for (unsigned int t = blockIdx.x; t < tiles; t += blocks) {
             move_tile_once<P, VLt, VSt, LA, LB, true>(static_cast<P*>(dst),
                                                       static_cast<const P*>(src), tp, tile, t);
             __syncthreads();  // the tile's LDS is rewritten by the next one
@@ -695,7 +706,7 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
       }
     }
   }
-  move_tiled<P>(dst, src, p, lds);
+  move_tiled<P>(dst, src, p, lds, blocks);
 }
 
 
@@ -705,9 +716,9 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
 // block sizes, and plans the row walk cannot take, decode per element.
 template <typename P>
 __device__ __forceinline__ void move_rows_entry(void* dst, const void* src, const MovePlan& p,
-                                                unsigned char* lds) {
-  if (blockDim.x != static_cast<unsigned>(kBlock) || gridDim.x > (1u << 23)) {
-    move_rows<P, 0>(dst, src, p);
+                                                unsigned char* lds, unsigned int blocks) {
+  if (blockDim.x != static_cast<unsigned>(kBlock) || blocks > (1u << 23)) {
+    move_rows<P, 0>(dst, src, p, blocks);
     return;
   }
   RowPlan* shared_rp = reinterpret_cast<RowPlan*>(lds);
@@ -719,29 +730,29 @@ __device__ __forceinline__ void move_rows_entry(void* dst, const void* src, cons
   }
   __syncthreads();
   if (!rows_ok) {
-    move_rows<P, 0>(dst, src, p);
+    move_rows<P, 0>(dst, src, p, blocks);
     return;
   }
   const RowPlan rp = uniform_copy(*shared_rp);
   constexpr int V = sizeof(P) == 1 ? 16 : sizeof(P) == 4 ? 4 : sizeof(P) == 8 ? 2 : 1;
   const bool vec = V > 1 && p.row_len == static_cast<long long>(rp.vpr) * V;
   if (vec && rp.reread)
-    move_row_units<P, V, false, -1>(dst, src, rp, gridDim.x);
+    move_row_units<P, V, false, -1>(dst, src, rp, blocks);
   else if (vec)
-    move_row_units<P, V, true, -1>(dst, src, rp, gridDim.x);
+    move_row_units<P, V, true, -1>(dst, src, rp, blocks);
   else if (rp.reread)
-    move_row_units<P, 1, false, -1>(dst, src, rp, gridDim.x);
+    move_row_units<P, 1, false, -1>(dst, src, rp, blocks);
   else
-    move_row_units<P, 1, true, -1>(dst, src, rp, gridDim.x);
+    move_row_units<P, 1, true, -1>(dst, src, rp, blocks);
 }
 
 template <typename P>
 __device__ __forceinline__ void move_dispatch(void* dst, const void* src, const MovePlan& p,
-                                              unsigned char* lds) {
+                                              unsigned char* lds, unsigned int blocks) {
   switch (p.mode) {
-    case kMoveTiled: move_tiled_entry<P>(dst, src, p, lds); break;
-    case kMoveContig: move_rows_entry<P>(dst, src, p, lds); break;
-    case kMoveGeneric: move_elements<P, 0>(dst, src, p); break;
+    case kMoveTiled: move_tiled_entry<P>(dst, src, p, lds, blocks); break;
+    case kMoveContig: move_rows_entry<P>(dst, src, p, lds, blocks); break;
+    case kMoveGeneric: move_elements<P, 0>(dst, src, p, blocks); break;
     default: break;
   }
 }
@@ -752,15 +763,17 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
                                            long long len) {
   const int es = dtype_size(dtype);
   if (es == 0) return;  // unknown tag: no work (reference c-kernel-abi.md:107-108)
+  if (entry_block_idle()) return;
+  const unsigned int blocks = entry_blocks();
   __shared__ MovePlan plan;
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
   if (threadIdx.x == 0) move_plan(&plan, src_layout, dst_strides, dst_offset, len, es);
   __syncthreads();
   switch (es) {
-    case 1: move_dispatch<uint8_t>(dst, src, plan, lds); break;
-    case 4: move_dispatch<uint32_t>(dst, src, plan, lds); break;
-    case 8: move_dispatch<unsigned long long>(dst, src, plan, lds); break;
-    case 16: move_dispatch<Elem16>(dst, src, plan, lds); break;
+    case 1: move_dispatch<uint8_t>(dst, src, plan, lds, blocks); break;
+    case 4: move_dispatch<uint32_t>(dst, src, plan, lds, blocks); break;
+    case 8: move_dispatch<unsigned long long>(dst, src, plan, lds, blocks); break;
+    case 16: move_dispatch<Elem16>(dst, src, plan, lds, blocks); break;
     default: break;
   }
 }
@@ -775,10 +788,11 @@ template <typename P>
 __device__ __forceinline__ void move_elements_wide(void* dst, const void* src, int n,
                                                    const long long* fe, const long long* fs,
                                                    const long long* fd, long long src_offset,
-                                                   long long dst_offset, long long len) {
+                                                   long long dst_offset, long long len,
+                                                   unsigned int blocks) {
   P* d = static_cast<P*>(dst);
   const P* s = static_cast<const P*>(src);
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  const long long gstride = static_cast<long long>(blocks) * blockDim.x;
   for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < len;
        f += gstride) {
     long long rest = f;
@@ -805,6 +819,8 @@ __device__ __forceinline__ void move_entry_by(void* dst, const void* src, int dt
                                               long long dst_offset, long long len) {
   const int es = dtype_size(dtype);
   if (es == 0 || len <= 0 || !ok || rank < 0) return;
+  if (entry_block_idle()) return;
+  const unsigned int blocks = entry_blocks();
   __shared__ MovePlan plan;
   __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
   __shared__ int fused;
@@ -821,9 +837,9 @@ __device__ __forceinline__ void move_entry_by(void* dst, const void* src, int dt
   auto run = [&](auto* tag) {
     using P = std::remove_pointer_t<decltype(tag)>;
     if (fused <= kMaxDims) {
-      move_dispatch<P>(dst, src, plan, lds);
+      move_dispatch<P>(dst, src, plan, lds, blocks);
     } else {
-      move_elements_wide<P>(dst, src, fused, fe, fs, fd, src_offset, dst_offset, count);
+      move_elements_wide<P>(dst, src, fused, fe, fs, fd, src_offset, dst_offset, count, blocks);
     }
   };
   switch (es) {
@@ -959,9 +975,9 @@ __device__ __forceinline__ void fill_view_body(void* out, const FillPlan& fp, un
 template <typename P>
 __device__ __forceinline__ void fill_view_wide(void* out, int n, const long long* fe,
                                                const long long* fs, long long offset,
-                                               long long len) {
+                                               long long len, unsigned int blocks) {
   P* o = static_cast<P*>(out);
-  const long long gstride = static_cast<long long>(gridDim.x) * blockDim.x;
+  const long long gstride = static_cast<long long>(blocks) * blockDim.x;
   for (long long f = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; f < len;
        f += gstride) {
     long long rest = f;
@@ -982,6 +998,8 @@ __device__ __forceinline__ void fill_view_entry(void* out, int dtype, int rank, 
                                                 long long len) {
   const int es = dtype_size(dtype);
   if (es == 0 || len <= 0 || rank < 0) return;
+  if (entry_block_idle()) return;
+  const unsigned int blocks = entry_blocks();
   __shared__ FillPlan plan;
   __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
   __shared__ int fused;
@@ -997,12 +1015,12 @@ __device__ __forceinline__ void fill_view_entry(void* out, int dtype, int rank, 
     using P = std::remove_pointer_t<decltype(tag)>;
     constexpr int V = sizeof(P) <= 8 && sizeof(P) >= 4 ? 16 / static_cast<int>(sizeof(P)) : 1;
     if (fused > kMaxDims) {
-      fill_view_wide<P>(out, fused, fe, fs, offset, count);
+      fill_view_wide<P>(out, fused, fe, fs, offset, count, blocks);
     } else if (V > 1 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                fill_vectorizable(plan, V)) {
-      fill_view_body<P, V, 0>(out, plan, gridDim.x);
+      fill_view_body<P, V, 0>(out, plan, blocks);
     } else {
-      fill_view_body<P, 1, 0>(out, plan, gridDim.x);
+      fill_view_body<P, 1, 0>(out, plan, blocks);
     }
   };
   switch (es) {
@@ -1036,7 +1054,7 @@ template <typename P, int VL, int VS>
 __global__ void __launch_bounds__(256)
     move_tiled_kernel(void* dst, const void* src, MovePlan plan) {
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
-  move_tiled_as<P, VL, VS>(dst, src, plan, lds);
+  move_tiled_as<P, VL, VS, true>(dst, src, plan, lds, gridDim.x);
 }
 
 template <typename P, int BS>
@@ -1070,9 +1088,9 @@ __global__ void __launch_bounds__(kBlock)
 template <typename P, int BS>
 __global__ void __launch_bounds__(256) move_flat_kernel(void* dst, const void* src, MovePlan plan) {
   if (plan.mode == kMoveContig) {
-    move_rows<P, BS>(dst, src, plan);
+    move_rows<P, BS>(dst, src, plan, gridDim.x);
   } else {
-    move_elements<P, BS>(dst, src, plan);
+    move_elements<P, BS>(dst, src, plan, gridDim.x);
   }
 }
 

@@ -370,8 +370,10 @@ int plan_strided(int dtype, const View& src, long long src_len, const View& dst,
 // reproduces those dims. False when more than 7 non-axis dims remain.
 bool reduction_pair(const View& out, const View& in, unsigned axis, t4a_cuda_layout* o8,
                     t4a_cuda_layout* i8, int* axis8) {
+  t4a::ReduceDimsN<t4a::kMaxDims - 1> work;
   return t4a::reduction_pair_view(in.rank, out.offset, out.extents, out.strides, in.offset,
-                                  in.extents, in.strides, static_cast<int>(axis), o8, i8, axis8);
+                                  in.extents, in.strides, static_cast<int>(axis), o8, i8, axis8,
+                                  &work);
 }
 
 // Reference plan_reduce (src/lib.rs:3318-3338) with check_reduce_width and

@@ -114,11 +114,11 @@ __device__ __forceinline__ void decode_output(const RD& rd, long long o, long lo
 template <typename Fold, typename T, bool Vector, int BS, typename RD>
 __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __restrict__ in,
                                              const RD& rd, long long output_len,
-                                             Fold f) {
+                                             Fold f, unsigned int blocks) {
   const long long len = rd.axis_len;
   const long long stride = rd.axis_stride;
   const int bs = block_threads<BS>();
-  const long long gstride = static_cast<long long>(gridDim.x) * bs;
+  const long long gstride = static_cast<long long>(blocks) * bs;
   for (long long o = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; o < output_len;
        o += gstride) {
     long long ib, ob;
@@ -188,40 +188,43 @@ __device__ __forceinline__ void unit_outputs(T* __restrict__ out, const T* __res
   }
 }
 
-// UNIT over a one-group axis (unit_one_group) in kBlock blocks: each thread
-// takes outputs o, o + G, o + 2G, o + 3G (G the grid's thread count), issues
-// their 16-byte loads together, then folds each output serially from element 0.
+// UNIT over a one-group axis (unit_one_group) in kBlock blocks: each wavefront
+// takes runs of 64 * U consecutive outputs (U = kUnitOutputsPerThread), lane l
+// the outputs run + l + 64u, issues their 16-byte loads together, then folds
+// each output serially from element 0.
 template <typename Fold, typename T, typename RD>
 __device__ __forceinline__ void unit_outputs_grouped(T* __restrict__ out,
                                                      const T* __restrict__ in,
                                                      const RD& rd, long long output_len,
-                                                     Fold f) {
+                                                     Fold f, unsigned int blocks) {
   constexpr int V = VecLanes<T>::value;
   constexpr int U = kUnitOutputsPerThread;
+  constexpr long long kRun = static_cast<long long>(kWave) * U;
   const long long len = rd.axis_len;
-  const long long gstride = static_cast<long long>(gridDim.x) * kBlock;
-  for (long long o0 = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; o0 < output_len;
-       o0 += U * gstride) {
+  const int lane = threadIdx.x % kWave;
+  const long long wave = (static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
+  const long long run_stride = static_cast<long long>(blocks) * (kBlock / kWave) * kRun;
+  for (long long run = wave * kRun; run < output_len; run += run_stride) {
     Group<T, V> g[U];
     long long ob[U];
     const T* xs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const long long o = o0 + u * gstride;
+      const long long o = run + lane + static_cast<long long>(kWave) * u;
       long long ib;
-      decode_output(rd, o < output_len ? o : o0, &ib, &ob[u]);  // past the end: o0 again
+      decode_output(rd, o < output_len ? o : run, &ib, &ob[u]);  // past the end: the run's first
       xs[u] = in + ib;
       const Vec<T, V> x = nt_load<T, V>(xs[u]);
       __builtin_memcpy(&g[u], &x, sizeof(g[u]));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (o0 + u * gstride < output_len) {
+      if (run + lane + static_cast<long long>(kWave) * u < output_len) {
         T acc = f.seed(g[u].x[0]);
 #pragma unroll
         for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
         for (long long i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
-        out[ob[u]] = acc;
+        nt_store<T, 1>(out + ob[u], Vec<T, 1>{{acc}});
       }
     }
   }
@@ -229,26 +232,35 @@ __device__ __forceinline__ void unit_outputs_grouped(T* __restrict__ out,
 
 template <typename Fold, typename T, int BS, typename RD>
 __device__ __forceinline__ void unit_body(void* out, const void* in, const RD& rd,
-                                          long long output_len, Fold f) {
+                                          long long output_len, Fold f, unsigned int blocks) {
   T* o = static_cast<T*>(out);
   const T* x = static_cast<const T*>(in);
   if constexpr (VecLanes<T>::value > 0) {
     constexpr int V = VecLanes<T>::value;
     bool vector = rd.axis_stride == 1 && rd.axis_len >= V && rd.in_offset % V == 0 &&
                   (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-    for (int k = 0; k < rd.n; ++k) vector = vector && rd.is[k] % V == 0;
+    // Compile-time subscripts for a by-value plan (a runtime one would copy the
+    // plan into per-lane scratch memory); the wide plans live in LDS.
+    if constexpr (RD::kDims <= kMaxDims) {
+#pragma unroll
+      for (int k = 0; k < RD::kDims; ++k) {
+        if (k < rd.n) vector = vector && rd.is[k] % V == 0;
+      }
+    } else {
+      for (int k = 0; k < rd.n; ++k) vector = vector && rd.is[k] % V == 0;
+    }
     if (vector) {
       if constexpr (BS == kBlock) {
         if (rd.axis_len < 2 * V) {
-          unit_outputs_grouped<Fold, T>(o, x, rd, output_len, f);
+          unit_outputs_grouped<Fold, T>(o, x, rd, output_len, f, blocks);
           return;
         }
       }
-      unit_outputs<Fold, T, true, BS>(o, x, rd, output_len, f);
+      unit_outputs<Fold, T, true, BS>(o, x, rd, output_len, f, blocks);
       return;
     }
   }
-  unit_outputs<Fold, T, false, BS>(o, x, rd, output_len, f);
+  unit_outputs<Fold, T, false, BS>(o, x, rd, output_len, f, blocks);
 }
 
 // ---- t4a_cuda_reduce: UNIT on a compact plan ----------------------------------------
@@ -293,30 +305,35 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
     if (up.vector) {
       if constexpr (BS == kBlock) {
         if (len < 2 * V) {
-          // one group per output: four outputs a grid-stride apart per thread
+          // One group per output: runs of 64 * U consecutive outputs a
+          // wavefront, lane l the outputs run + l + 64u (unit_outputs_grouped's
+          // walk with 32-bit indices).
           constexpr int U = kUnitOutputsPerThread;
-          for (unsigned int o0 = blockIdx.x * BS + threadIdx.x; o0 < output_len;
-               o0 += U * gstride) {
+          constexpr unsigned int kRun = kWave * U;
+          const unsigned int lane = threadIdx.x % kWave;
+          const unsigned int wave = (blockIdx.x * BS + threadIdx.x) / kWave;
+          const unsigned int run_stride = gstride / kWave * kRun;
+          for (unsigned int run = wave * kRun; run < output_len; run += run_stride) {
             Group<T, V> g[U];
             long long ob[U];
             const T* xs[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-              const unsigned int o = o0 + u * gstride;
+              const unsigned int o = run + lane + kWave * u;
               long long ib;
-              unit_decode(up, o < output_len ? o : o0, &ib, &ob[u]);
+              unit_decode(up, o < output_len ? o : run, &ib, &ob[u]);
               xs[u] = in + ib;
               const Vec<T, V> x = nt_load<T, V>(xs[u]);
               __builtin_memcpy(&g[u], &x, sizeof(g[u]));
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-              if (o0 + u * gstride < output_len) {
+              if (run + lane + kWave * u < output_len) {
                 T acc = f.seed(g[u].x[0]);
 #pragma unroll
                 for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
                 for (int i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
-                out[ob[u]] = acc;
+                nt_store<T, 1>(out + ob[u], Vec<T, 1>{{acc}});
               }
             }
           }
@@ -407,7 +424,8 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
 // first W / 32 lanes (reference reduce.cu:170-194).
 template <typename Fold, typename T, typename RD>
 __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, const RD& rd,
-                                           long long output_len, Fold f, unsigned char* lds) {
+                                           long long output_len, Fold f, unsigned char* lds,
+                                           unsigned int blocks) {
   T* out = static_cast<T*>(out_ptr);
   const T* in = static_cast<const T*>(in_ptr);
   T* warp_results = reinterpret_cast<T*>(lds);
@@ -415,7 +433,7 @@ __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, co
   const int lane = threadIdx.x;
   const long long len = rd.axis_len;
   const long long stride = rd.axis_stride;
-  for (long long o = blockIdx.x; o < output_len; o += gridDim.x) {
+  for (long long o = blockIdx.x; o < output_len; o += blocks) {
     long long ib, ob;
     decode_output(rd, o, &ib, &ob);
     const T* x = in + ib;
@@ -423,7 +441,9 @@ __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, co
     // A plane holds len >= w elements. When a lane walks at most kAhead of them
     // (the combine passes: 8 partials a lane for 4096 splits at W = 512), every
     // load is issued before the first fold, one memory round trip per output.
-    constexpr int kAhead = 16;
+    // kAhead holds 64 bytes of elements (16 f32, 8 f64 or c32, 4 c64): more
+    // would set the register budget of every kernel that carries this body.
+    constexpr int kAhead = sizeof(T) >= 16 ? 4 : sizeof(T) >= 8 ? 8 : 16;
     if (len <= static_cast<long long>(w) * kAhead) {
       T v[kAhead];
 #pragma unroll
@@ -887,7 +907,7 @@ template <typename Fold, typename T, typename RD>
 __device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const void* in_ptr,
                                                      const RD& rd, long long output_len,
                                                      long long splits, long long chunk_len,
-                                                     Fold f) {
+                                                     Fold f, unsigned int blocks) {
   T* partials = static_cast<T*>(partials_ptr);
   const T* in = static_cast<const T*>(in_ptr);
   const int w = blockDim.x <= static_cast<unsigned>(kWarp) ? static_cast<int>(blockDim.x) : kWarp;
@@ -900,7 +920,7 @@ __device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const v
   // so a block's planes read neighbouring columns of the same rows.
   const bool split_major = rd.axis_stride != 1;
   for (long long idx = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
-       idx < cubes; idx += static_cast<long long>(gridDim.x) * planes) {
+       idx < cubes; idx += static_cast<long long>(blocks) * planes) {
     long long o, split;
     if (split_major) {
       split = idx / output_len;
@@ -923,9 +943,10 @@ __device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const v
 template <typename Fold, typename T>
 __device__ __forceinline__ void partials_planes(void* partials_ptr, const void* in_ptr,
                                                 const PartialsPlan& pp, long long output_len,
-                                                long long splits, long long chunk_len, Fold f) {
+                                                long long splits, long long chunk_len, Fold f,
+                                                unsigned int blocks) {
   partials_planes_dims<Fold, T>(partials_ptr, in_ptr, pp.dims, output_len, splits, chunk_len,
-                                f);
+                                f, blocks);
 }
 
 // Unit `u` of the COLUMNS/ROWS mappings: column block fastest, then the split,
@@ -1047,7 +1068,8 @@ __device__ __forceinline__ void side_unit(const SidePlan& sp, unsigned int u,
 // own-left xor tree.
 template <typename Fold, typename T, int CPL>
 __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* in_ptr,
-                                               const SidePlan& sp, Fold f, T* lds, int* redo) {
+                                               const SidePlan& sp, Fold f, T* lds, int* redo,
+                                               unsigned int blocks) {
   constexpr int kWaves = kBlock / kWave;
   constexpr int kLanesPerWave = kWarp / kWaves;  // plane lanes per wavefront: 8
   constexpr int BC = kWave * CPL;                // columns per block
@@ -1061,7 +1083,7 @@ __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* i
   const int t = threadIdx.x % kWave;
   const long long row_bytes = sp.axis_stride * static_cast<long long>(sizeof(T));
   const long long lane_off = static_cast<long long>(t) * CPL * static_cast<long long>(sizeof(T));
-  for (long long u = blockIdx.x; u < sp.units; u += gridDim.x) {
+  for (long long u = blockIdx.x; u < sp.units; u += blocks) {
     unsigned int block;
     long long ib, pb;
     int len;
@@ -1299,21 +1321,6 @@ __device__ __forceinline__ void dispatch_fold(int op, Fn&& fn) {
   }
 }
 
-// A value every lane holds alike, read out of LDS into scalar registers (one
-// readfirstlane per dword), so that a loop reads it without LDS traffic.
-template <typename T>
-__device__ __forceinline__ T uniform_copy(const T& shared_value) {
-  static_assert(sizeof(T) % 4 == 0, "whole dwords");
-  unsigned int words[sizeof(T) / 4];
-  __builtin_memcpy(words, &shared_value, sizeof(T));
-#pragma unroll
-  for (int i = 0; i < static_cast<int>(sizeof(T) / 4); ++i)
-    words[i] = __builtin_amdgcn_readfirstlane(words[i]);
-  T out;
-  __builtin_memcpy(&out, words, sizeof(T));
-  return out;
-}
-
 template <typename Fn>
 __device__ __forceinline__ void dispatch_dtype(int dtype, Fn&& fn) {
   switch (dtype) {
@@ -1330,12 +1337,12 @@ __device__ __forceinline__ void dispatch_dtype(int dtype, Fn&& fn) {
 template <typename T, typename RD>
 __device__ __forceinline__ void reduce_run(void* out, const void* in, int op, bool plane,
                                            const RD& rd, long long output_len,
-                                           unsigned char* warp_lds) {
+                                           unsigned char* warp_lds, unsigned int blocks) {
   dispatch_fold<T>(op, [&](auto fold) {
     if (plane) {
-      plane_body<decltype(fold), T>(out, in, rd, output_len, fold, warp_lds);
+      plane_body<decltype(fold), T>(out, in, rd, output_len, fold, warp_lds, blocks);
     } else {
-      unit_body<decltype(fold), T, 0>(out, in, rd, output_len, fold);
+      unit_body<decltype(fold), T, 0>(out, in, rd, output_len, fold, blocks);
     }
   });
 }
@@ -1348,7 +1355,8 @@ __global__ void __launch_bounds__(512)
     reduce_kernel(void* out, const void* in, int op, int strategy, ReduceDims rd,
                   long long output_len) {
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(T)];
-  reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds);
+  reduce_run<T>(out, in, op, strategy == T4A_CUDA_REDUCE_PLANE, rd, output_len, warp_lds,
+                gridDim.x);
 }
 
 // UNIT on a compact plan, one kernel per (element type, fold, block size).
@@ -1367,7 +1375,8 @@ template <typename T, typename Fold>
 __global__ void __launch_bounds__(512)
     reduce_plane_lean_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len) {
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(T)];
-  plane_body<Fold, T>(out, in, up, static_cast<long long>(output_len), Fold{}, warp_lds);
+  plane_body<Fold, T>(out, in, up, static_cast<long long>(output_len), Fold{}, warp_lds,
+                      gridDim.x);
 }
 
 // UNIT with the planner's blocks of BS threads.
@@ -1375,7 +1384,7 @@ template <typename T, int BS>
 __global__ void __launch_bounds__(BS)
     reduce_unit_kernel(void* out, const void* in, int op, ReduceDims rd, long long output_len) {
   dispatch_fold<T>(op, [&](auto fold) {
-    unit_body<decltype(fold), T, BS>(out, in, rd, output_len, fold);
+    unit_body<decltype(fold), T, BS>(out, in, rd, output_len, fold, gridDim.x);
   });
 }
 
@@ -1384,7 +1393,8 @@ __global__ void __launch_bounds__(256)
     partials_plane_kernel(void* partials, const void* in, int op, PartialsPlan pp,
                           long long output_len, long long splits, long long chunk_len) {
   dispatch_fold<T>(op, [&](auto fold) {
-    partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len, fold);
+    partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len, fold,
+                                       gridDim.x);
   });
 }
 
@@ -1425,7 +1435,7 @@ __global__ void __launch_bounds__(kBlock)
   __shared__ T lds[(kBlock / kWave) * kWave * CPL];
   __shared__ int redo;
   dispatch_fold<T>(op, [&](auto fold) {
-    partials_tiles<decltype(fold), T, CPL>(partials, in, sp, fold, lds, &redo);
+    partials_tiles<decltype(fold), T, CPL>(partials, in, sp, fold, lds, &redo, gridDim.x);
   });
 }
 
@@ -1459,6 +1469,8 @@ extern "C" __global__ void __launch_bounds__(512)
     t4a_cuda_reduce(void* out, const void* in, int dtype, int op, int strategy,
                     t4a_cuda_layout out_layout, t4a_cuda_layout in_layout, int axis,
                     long long output_len) {
+  if (t4a::entry_block_idle()) return;
+  const unsigned int blocks = t4a::entry_blocks();
   __shared__ t4a::ReduceDims rd;
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
   if (threadIdx.x == 0) t4a::reduce_dims(&rd, out_layout, in_layout, axis);
@@ -1466,7 +1478,7 @@ extern "C" __global__ void __launch_bounds__(512)
   const bool plane = strategy == T4A_CUDA_REDUCE_PLANE;
   t4a::dispatch_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
-    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds);
+    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds, blocks);
   });
 }
 
@@ -1475,6 +1487,8 @@ extern "C" __global__ void __launch_bounds__(256)
                              t4a_cuda_layout partials_layout, t4a_cuda_layout in_layout,
                              int axis, long long output_len, long long splits,
                              long long chunk_len) {
+  if (t4a::entry_block_idle()) return;
+  const unsigned int blocks = t4a::entry_blocks();
   __shared__ t4a::PartialsPlan pp;
   if (threadIdx.x == 0) {
     const int w = blockDim.x <= 32u ? static_cast<int>(blockDim.x) : t4a::kWarp;
@@ -1486,7 +1500,7 @@ extern "C" __global__ void __launch_bounds__(256)
     using T = std::remove_pointer_t<decltype(tag)>;
     t4a::dispatch_fold<T>(op, [&](auto fold) {
       t4a::partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
-                                              fold);
+                                              fold, blocks);
     });
   });
 }
@@ -1511,6 +1525,8 @@ extern "C" __global__ void __launch_bounds__(512)
     t4a_cuda_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
                         t4a_cuda_layout_any out_layout, t4a_cuda_layout_any in_layout, int axis,
                         long long output_len) {
+  if (t4a::entry_block_idle()) return;
+  const unsigned int blocks = t4a::entry_blocks();
   __shared__ t4a::ReduceDimsWide rd;
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
   if (threadIdx.x == 0) any_dims(&rd, out_layout, in_layout, axis);
@@ -1519,7 +1535,7 @@ extern "C" __global__ void __launch_bounds__(512)
   const bool plane = strategy == T4A_CUDA_REDUCE_PLANE;
   t4a::dispatch_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
-    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds);
+    t4a::reduce_run<T>(out, in, op, plane, rd, output_len, warp_lds, blocks);
   });
 }
 
@@ -1528,7 +1544,18 @@ extern "C" __global__ void __launch_bounds__(512)
 // pair the host planner plans with (reduction_pair_view), plans pass 1 as the
 // by-value launcher does, and keeps the SidePlan when that plan is TILES
 // (returning its columns per lane, 0 otherwise).
-__device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, int dtype, const void* in,
+// Thread 0's planning temporaries of the general-rank pass 1, in LDS: as
+// locals, their runtime-subscripted arrays would take per-lane scratch memory,
+// which every dispatch of the kernel would pay for.
+struct AnySideScratch {
+  t4a_cuda_layout p8, i8;
+  t4a::PartialsPlan pp;
+  t4a::ReduceDimsN<t4a::kMaxDims - 1> fused;
+  int axis8;
+};
+
+__device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, AnySideScratch* tmp,
+                                             int dtype, const void* in,
                                              const t4a_cuda_layout_any& partials,
                                              const t4a_cuda_layout_any& input, int axis,
                                              long long output_len, long long splits,
@@ -1536,20 +1563,18 @@ __device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, int dtype, con
   if (!t4a::sideways_dtype(dtype) || axis < 0 || axis >= input.rank ||
       partials.rank != input.rank)
     return 0;
-  t4a_cuda_layout p8, i8;
-  int axis8;
   if (!t4a::reduction_pair_view(input.rank, partials.offset, partials.extents, partials.strides,
-                                input.offset, input.extents, input.strides, axis, &p8, &i8,
-                                &axis8))
+                                input.offset, input.extents, input.strides, axis, &tmp->p8,
+                                &tmp->i8, &tmp->axis8, &tmp->fused))
     return 0;
+  const int axis8 = tmp->axis8;
   const uintptr_t address = reinterpret_cast<uintptr_t>(in);
   const int align = (address & 15) == 0 ? 16 : (address & 7) == 0 ? 8 : (address & 3) == 0 ? 4 : 1;
-  t4a::PartialsPlan pp;
-  t4a::partials_plan(&pp, p8, i8, axis8, output_len, splits, t4a::kWarp, 1,
+  t4a::partials_plan(&tmp->pp, tmp->p8, tmp->i8, axis8, output_len, splits, t4a::kWarp, 1,
                      t4a::dtype_size(dtype), align);
-  if (pp.mode != t4a::kPartialsTiles) return 0;
-  *side = t4a::side_plan(pp, splits, chunk_len);
-  return pp.cpl;
+  if (tmp->pp.mode != t4a::kPartialsTiles) return 0;
+  *side = t4a::side_plan(tmp->pp, splits, chunk_len);
+  return tmp->pp.cpl;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
@@ -1559,23 +1584,26 @@ extern "C" __global__ void __launch_bounds__(256)
                                  long long splits, long long chunk_len) {
   __shared__ t4a::ReduceDimsWide rd;
   __shared__ t4a::SidePlan side;
+  __shared__ AnySideScratch side_tmp;
   __shared__ int side_cpl;
   __shared__ alignas(16) unsigned char tiles_lds[(t4a::kBlock / t4a::kWave) * t4a::kWave * 2 * 8];
   __shared__ int redo;
+  if (t4a::entry_block_idle()) return;
+  const unsigned int blocks = t4a::entry_blocks();
   const bool whole_waves = blockDim.x == static_cast<unsigned>(t4a::kBlock) &&
                            blockDim.y == 1 && blockDim.z == 1;
   if (threadIdx.x == 0) {
     any_dims(&rd, partials_layout, in_layout, axis);
     // Only a strided axis can take the column mapping.
     side_cpl = rd.n >= 0 && whole_waves && rd.axis_stride != 1
-                   ? any_side_plan(&side, dtype, in, partials_layout, in_layout, axis,
-                                   output_len, splits, chunk_len)
+                   ? any_side_plan(&side, &side_tmp, dtype, in, partials_layout, in_layout,
+                                   axis, output_len, splits, chunk_len)
                    : 0;
   }
   __syncthreads();
   if (rd.n < 0) return;
   if (side_cpl > 0) {
-    const t4a::SidePlan sp = t4a::uniform_copy(side);
+    const t4a::SidePlan& sp = side;  // from LDS (copied to scalar registers it spills)
     const int cpl = side_cpl;
     t4a::dispatch_dtype(dtype, [&](auto* tag) {
       using T = std::remove_pointer_t<decltype(tag)>;
@@ -1583,9 +1611,9 @@ extern "C" __global__ void __launch_bounds__(256)
         T* lds = reinterpret_cast<T*>(tiles_lds);
         t4a::dispatch_fold<T>(op, [&](auto fold) {
           if (cpl == 2)
-            t4a::partials_tiles<decltype(fold), T, 2>(partials, in, sp, fold, lds, &redo);
+            t4a::partials_tiles<decltype(fold), T, 2>(partials, in, sp, fold, lds, &redo, blocks);
           else
-            t4a::partials_tiles<decltype(fold), T, 1>(partials, in, sp, fold, lds, &redo);
+            t4a::partials_tiles<decltype(fold), T, 1>(partials, in, sp, fold, lds, &redo, blocks);
         });
       }
     });
@@ -1595,7 +1623,7 @@ extern "C" __global__ void __launch_bounds__(256)
     using T = std::remove_pointer_t<decltype(tag)>;
     t4a::dispatch_fold<T>(op, [&](auto fold) {
       t4a::partials_planes_dims<decltype(fold), T>(partials, in, rd, output_len, splits,
-                                                   chunk_len, fold);
+                                                   chunk_len, fold, blocks);
     });
   });
 }
