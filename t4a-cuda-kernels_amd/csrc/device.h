@@ -41,21 +41,31 @@ __device__ __forceinline__ int block_threads() {
 // kEntryWaves wavefronts' worth of blocks of the grid's first row working
 // (blocks past that, and blocks off the first row, return before planning),
 // and the kept blocks walk all of the work with their own count as the grid
-// stride. 2048 wavefronts (512 blocks of 256 threads) fill about half of what
-// the entries' registers and LDS let the chip hold, so the returning blocks
-// pass through the remaining slots while the working ones stream; a cap at
-// full residency would hold them back until the work is done.
-constexpr unsigned int kEntryWaves = 2048;
+// stride. The movement entries keep 2048 wavefronts (512 blocks of 256
+// threads): about half of what their registers and LDS let the chip hold, so
+// the returning blocks pass through the remaining slots while the working
+// ones stream (a cap at full residency measured slower: the returning blocks
+// then wait for the work to finish). The reduction entries keep 8192, the
+// chip's whole wavefront capacity: their plane walks wait on each cube's
+// loads in turn, so every working plane adds loads in flight, and their
+// planning is a few dozen instructions.
+constexpr unsigned int kMoveEntryWaves = 2048;
+constexpr unsigned int kReduceEntryWaves = 8192;
 
-__device__ __forceinline__ unsigned int entry_blocks() {
+// The launchers' persistent tile walk takes as many blocks as the device
+// holds at once; this is the count for MI355X (256 CUs x 8 blocks of 256
+// threads) when the runtime cannot be asked.
+constexpr unsigned int kTileWalkBlocks = 2048;
+
+__device__ __forceinline__ unsigned int entry_blocks(unsigned int waves) {
   const unsigned int waves_per_block = (blockDim.x * blockDim.y * blockDim.z + 63u) / 64u;
-  unsigned int cap = kEntryWaves / (waves_per_block ? waves_per_block : 1u);
+  unsigned int cap = waves / (waves_per_block ? waves_per_block : 1u);
   if (cap == 0) cap = 1;
   return gridDim.x < cap ? gridDim.x : cap;
 }
 
-__device__ __forceinline__ bool entry_block_idle() {
-  return blockIdx.y != 0 || blockIdx.z != 0 || blockIdx.x >= entry_blocks();
+__device__ __forceinline__ bool entry_block_idle(unsigned int waves) {
+  return blockIdx.y != 0 || blockIdx.z != 0 || blockIdx.x >= entry_blocks(waves);
 }
 
 using c32 = t4a_cuda_c32;

@@ -613,12 +613,20 @@ T4A_HD bool fill_vectorizable(const FillPlan& p, int v) {
   return true;
 }
 
-// The one-tile-per-block form of a TILED plan: a block moves tile blockIdx.x
-// whole, all of a thread's loads issued before its first LDS write, the tile
-// shape a compile-time LA x LB. It applies when each chain has at most two
-// dims (an inner one at full extent, the tiled outer one), the tile count is
-// below 2^30 (32-bit coordinates) and (la, lb) is one of the shapes below.
-struct TilePlan {
+// The TilePlan form of a TILED plan: tile t decoded from its index by
+// precomputed divisors and moved whole, all of a thread's loads issued before
+// its first LDS write, the tile shape a compile-time LA x LB. It applies when
+// each chain has at most two dims (an inner one at full extent, the tiled
+// outer one), the tile count is below 2^30 (32-bit coordinates) and (la, lb)
+// is one of the shapes below.
+// NC: the coordinate slots. The planner fills the full form (every fused dim
+// can be a batch coordinate); a plan of at most four coordinates (C3 and C5
+// have four) also travels in the compact form, whose 216 bytes of kernel
+// arguments leave the tile kernels scalar registers for eight wavefronts per
+// SIMD -- the full 384 bytes held them to seven.
+template <int NC>
+struct TilePlanN {
+  static constexpr int kCoords = NC;
   long long src_offset, dst_offset;
   long long a_ss0, a_ss1;  // source strides of the A chain's inner and outer dims
   long long b_ds0, b_ds1;  // destination strides of the B chain's inner and outer dims
@@ -627,10 +635,50 @@ struct TilePlan {
   unsigned int a_last, b_last;  // the outer dims' extents
   int ncoord;                   // coordinates of the tile walk: A tile, B tile, batch dims
   int skew_first, skew_second;  // diagonal order (see the persistent walk), -1 if none
-  FastDiv coord[kMaxDims + 2];
-  long long coord_ss[kMaxDims + 2];  // source / destination offset per unit of a coordinate
-  long long coord_ds[kMaxDims + 2];
+  FastDiv coord[NC];
+  long long coord_ss[NC];  // source / destination offset per unit of a coordinate
+  long long coord_ds[NC];
 };
+using TilePlan = TilePlanN<kMaxDims + 2>;
+constexpr int kCompactCoords = 4;
+using TilePlanCompact = TilePlanN<kCompactCoords>;
+
+// Whether the in-tile offsets of the valid slots -- the source offset of row
+// i plus a column, the destination offset of column j plus a row, for an LA x
+// LB tile of esize-byte elements -- span fewer than 2^31 bytes on each side.
+inline bool tile_offsets_narrow(const TilePlan& tp, int la, int lb, int esize) {
+  auto mag = [](long long v) { return v < 0 ? -static_cast<double>(v) : static_cast<double>(v); };
+  const double src = mag(tp.a_ss0) * (tp.a_in.d - 1.0) + mag(tp.a_ss1) * (tp.a_tile - 1.0) + lb;
+  const double dst = mag(tp.b_ds0) * (tp.b_in.d - 1.0) + mag(tp.b_ds1) * (tp.b_tile - 1.0) + la;
+  return src * esize < 2147483648.0 && dst * esize < 2147483648.0;
+}
+
+// The compact form of a plan of at most kCompactCoords coordinates.
+T4A_HD TilePlanCompact compact_tile_plan(const TilePlan& tp) {
+  TilePlanCompact c;
+  c.src_offset = tp.src_offset;
+  c.dst_offset = tp.dst_offset;
+  c.a_ss0 = tp.a_ss0;
+  c.a_ss1 = tp.a_ss1;
+  c.b_ds0 = tp.b_ds0;
+  c.b_ds1 = tp.b_ds1;
+  c.a_in = tp.a_in;
+  c.b_in = tp.b_in;
+  c.a_tile = tp.a_tile;
+  c.b_tile = tp.b_tile;
+  c.a_last = tp.a_last;
+  c.b_last = tp.b_last;
+  c.ncoord = tp.ncoord;
+  c.skew_first = tp.skew_first;
+  c.skew_second = tp.skew_second;
+  for (int q = 0; q < kCompactCoords; ++q) {
+    const bool used = q < tp.ncoord;
+    c.coord[q] = used ? tp.coord[q] : fast_div(1);
+    c.coord_ss[q] = used ? tp.coord_ss[q] : 0;
+    c.coord_ds[q] = used ? tp.coord_ds[q] : 0;
+  }
+  return c;
+}
 
 // Compile-time tile shapes, the planner's full tiles when both chains reach
 // their targets: 64 x 64 for 4-byte elements, 64 x 32 for 8-byte ones and

@@ -286,7 +286,7 @@ constexpr int max_tile_elems() {
 
 // `Pipelined`: with kTileThreads threads a block holds the next tile's loads in
 // registers while it stores the current one (the launchers' kernel); the
-// entries, which carry every plan's code in one kernel, take the one-tile-at-a-
+// entries, which carry every plan's code in one kernel, take the tile-at-a-
 // time walk, whose registers do not cap the occupancy of all their paths.
 template <typename P, int VL, int VS, bool Pipelined>
 __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restrict__ src,
@@ -377,34 +377,57 @@ __device__ __forceinline__ void move_tiles(P* __restrict__ dst, const P* __restr
   }
 }
 
-// One tile per block (TilePlan): the tile's coordinates from blockIdx.x by
-// precomputed divisors (uniform, scalar), then every load of the thread
-// issued before its first LDS write, as in the tiled transpose; element (i, j)
-// of the LA x LB tile sits at src_base + src_a(i) + j and dst_base + i +
-// dst_b(j), the chain offsets decoded per slot (at most two digits). A partial
-// tile's empty slots load the tile's first element instead (so no branch
-// separates the loads) and are neither parked nor stored.
-// `Walk`: the tile is `tile_index` (the entries' tile loop); otherwise
-// blockIdx.x, read directly (the launchers' kernel: taking it as an argument
-// changed the store loop's register allocation so that every LDS read waited
-// for all earlier stores, 4 % slower on C3).
-template <typename P, int VL, int VS, int LA, int LB, bool Walk = false>
-__device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __restrict__ src,
-                                               const TilePlan& tp, P* tile,
-                                               unsigned int tile_index) {
-  constexpr int BS = kBlock;
-  constexpr int PITCH = LB + 1;
-  constexpr int LBV = LB / VL;
-  constexpr int LAV = LA / VS;
-  constexpr int RL = LA * LBV / BS;
-  constexpr int RS = LB * LAV / BS;
-  static_assert(RL * BS == LA * LBV && RS * BS == LB * LAV, "the block divides the tile");
-  unsigned int rest = Walk ? tile_index : blockIdx.x;
-  unsigned int first = 0, ta = 0, tb = 0;
-  long long sb = tp.src_offset;
-  long long db = tp.dst_offset;
+// The TilePlan body: tile t's coordinates by precomputed divisors (uniform,
+// scalar), then every load of the thread issued before its first LDS write,
+// as in the tiled transpose; element (i, j) of the LA x LB tile sits at
+// src_base + src_a(i) + j and dst_base + i + dst_b(j), the chain offsets
+// decoded per slot (at most two digits). A partial tile's empty slots load
+// the tile's first element instead (so no branch separates the loads) and are
+// neither parked nor stored.
+// Where element (i, j) of the LA x LB tile sits in LDS. The
+// LDS serves a wave's 8-byte reads 32 lanes a pass over 64 banks of 4 bytes
+// and its 8-byte writes 16 lanes a pass over 32 banks (measured on gfx950
+// with SQ_LDS_BANK_CONFLICT over fixed lane patterns). Rows padded by one
+// element serve every access pattern of 4- and 16-byte elements without
+// conflict. For 8-byte elements (64 x 32) they do not: a 16-byte store vector
+// reads rows 2n and 2n + 1 of a column (n = 0..31 over 32 lanes), which the
+// pad puts on 16 bank pairs, two lanes each, and a 16-byte load vector (VL =
+// 2) writes columns 2m + k of a row (m = 0..15 over 16 lanes), on 8 bank
+// pairs mod 32: every such read and write took two passes. Those tiles are
+// unpadded: column j of row i sits at g(j) ^ (i % 32) ^ (i / 32), where g
+// interleaves the even columns before the odd ones when VL = 2 (identity
+// otherwise). The XOR term sends any 32 consecutive rows, and the 32 even and
+// the 32 odd rows, of a column to 32 distinct bank pairs; g puts the 16
+// columns 2m + k that 16 lanes write at once on 16 consecutive words.
+template <typename P, int LA, int LB, int VL>
+struct TileSlots {
+  static constexpr bool kSwizzled = sizeof(P) == 8 && LB == 32 && LA == 2 * LB;
+  static constexpr int kElems = kSwizzled ? LA * LB : LA * (LB + 1);
+  static __device__ __forceinline__ int at(int i, int j) {
+    if constexpr (kSwizzled) {
+      const int g = VL == 2 ? (j >> 1) | ((j & 1) << 4) : j;
+      return i * LB + (g ^ (i & (LB - 1)) ^ (i / LB));
+    } else {
+      return i * (LB + 1) + j;
+    }
+  }
+};
+
+// The source and destination bases of tile `t` and its valid extents (in
+// elements) along the A and B sides; uniform over the block.
+struct TileBase {
+  long long sb, db;
+  int va, vb;
+};
+
+template <typename TP>
+__device__ __forceinline__ TileBase tile_base(const TP& tp, unsigned int t) {
+  unsigned int rest = t, first = 0, ta = 0, tb = 0;
+  TileBase b;
+  b.sb = tp.src_offset;
+  b.db = tp.dst_offset;
 #pragma unroll
-  for (int q = 0; q < kMaxDims + 2; ++q) {
+  for (int q = 0; q < TP::kCoords; ++q) {
     if (q < tp.ncoord) {
       const unsigned int quot = div_by(rest, tp.coord[q]);
       unsigned int c = rest - quot * tp.coord[q].d;
@@ -416,58 +439,199 @@ __device__ __forceinline__ void move_tile_once(P* __restrict__ dst, const P* __r
       if (q == tp.skew_first) first = c;
       if (q == 0) ta = c;
       if (q == 1) tb = c;
-      sb += static_cast<long long>(c) * tp.coord_ss[q];
-      db += static_cast<long long>(c) * tp.coord_ds[q];
+      b.sb += static_cast<long long>(c) * tp.coord_ss[q];
+      b.db += static_cast<long long>(c) * tp.coord_ds[q];
     }
   }
   const unsigned int a_left = tp.a_last - ta * tp.a_tile;
   const unsigned int b_left = tp.b_last - tb * tp.b_tile;
-  const int va = static_cast<int>(tp.a_in.d * (a_left < tp.a_tile ? a_left : tp.a_tile));
-  const int vb = static_cast<int>(tp.b_in.d * (b_left < tp.b_tile ? b_left : tp.b_tile));
-  const P* s = src + sb;
-  P* d = dst + db;
+  b.va = static_cast<int>(tp.a_in.d * (a_left < tp.a_tile ? a_left : tp.a_tile));
+  b.vb = static_cast<int>(tp.b_in.d * (b_left < tp.b_tile ? b_left : tp.b_tile));
+  return b;
+}
+
+// Offset of tile row i from the tile's source base (the A chain's two digits
+// times their source strides), and of tile column j from its destination base.
+template <typename TP>
+__device__ __forceinline__ long long tile_src_a(const TP& tp, int i) {
+  const unsigned int o = div_by(static_cast<unsigned int>(i), tp.a_in);
+  return static_cast<long long>(i - static_cast<int>(o * tp.a_in.d)) * tp.a_ss0 +
+         static_cast<long long>(o) * tp.a_ss1;
+}
+template <typename TP>
+__device__ __forceinline__ long long tile_dst_b(const TP& tp, int j) {
+  const unsigned int o = div_by(static_cast<unsigned int>(j), tp.b_in);
+  return static_cast<long long>(j - static_cast<int>(o * tp.b_in.d)) * tp.b_ds0 +
+         static_cast<long long>(o) * tp.b_ds1;
+}
+
+// Persistent walk: the block moves tiles blockIdx.x, blockIdx.x + blocks, ...
+// and issues the next tile's loads before it stores the current tile from LDS
+// (so loads stay in flight through the store phase instead of waiting for a
+// new block: C5's permute in 97 us against 102 with a block per tile). Every
+// wave of a block takes the same branches (the tile count and bases are
+// uniform).
+// Each slot's offset inside a tile, the same for every tile, is computed once
+// per thread; `Narrow`: their byte span fits 31 bits (tile_offsets_narrow),
+// and each takes one register instead of two.
+// Not `Pipelined` (the entries, which carry every plan's code in one kernel
+// and whose occupancy the walk's registers would cap): one tile at a time,
+// loaded, parked and stored before the next, its offsets computed per tile.
+template <typename P, int VL, int VS, int LA, int LB, typename TP, bool Narrow,
+          bool Pipelined = true>
+__device__ __forceinline__ void move_tile_walk(P* __restrict__ dst, const P* __restrict__ src,
+                                               const TP& tp, P* tile, unsigned int tiles,
+                                               unsigned int blocks) {
+  constexpr int BS = kBlock;
+  using Slots = TileSlots<P, LA, LB, VL>;
+  constexpr int LBV = LB / VL;
+  constexpr int LAV = LA / VS;
+  constexpr int RL = LA * LBV / BS;
+  constexpr int RS = LB * LAV / BS;
+  static_assert(RL * BS == LA * LBV && RS * BS == LB * LAV, "the block divides the tile");
   const int tid = threadIdx.x;
-  auto src_a = [&](int i) {
-    const unsigned int o = div_by(static_cast<unsigned int>(i), tp.a_in);
-    return static_cast<long long>(i - static_cast<int>(o * tp.a_in.d)) * tp.a_ss0 +
-           static_cast<long long>(o) * tp.a_ss1;
-  };
-  auto dst_b = [&](int j) {
-    const unsigned int o = div_by(static_cast<unsigned int>(j), tp.b_in);
-    return static_cast<long long>(j - static_cast<int>(o * tp.b_in.d)) * tp.b_ds0 +
-           static_cast<long long>(o) * tp.b_ds1;
-  };
-  Vec<P, VL> x[RL];
+  if constexpr (!Pipelined) {
+    // The tile count is below 2^30 (tile_plan), so t + blocks cannot wrap.
+    for (unsigned int t = blockIdx.x; t < tiles; t += blocks) {
+      const TileBase b = tile_base(tp, t);
+      const P* s = src + b.sb;
+      P* d = dst + b.db;
+      Vec<P, VL> x[RL];
 #pragma unroll
-  for (int r = 0; r < RL; ++r) {
-    const int e = tid + r * BS;
-    const int i = e / LBV;
-    const int j = (e % LBV) * VL;
-    const bool valid = i < va && j < vb;
-    x[r] = nt_load<P, VL>(valid ? s + src_a(i) + j : s);
-  }
+      for (int r = 0; r < RL; ++r) {
+        const int e = tid + r * BS;
+        const int i = e / LBV;
+        const int j = (e % LBV) * VL;
+        x[r] = nt_load<P, VL>(i < b.va && j < b.vb ? s + tile_src_a(tp, i) + j : s);
+      }
 #pragma unroll
-  for (int r = 0; r < RL; ++r) {
-    const int e = tid + r * BS;
-    const int i = e / LBV;
-    const int j = (e % LBV) * VL;
-    if (i < va && j < vb) {
+      for (int r = 0; r < RL; ++r) {
+        const int e = tid + r * BS;
+        const int i = e / LBV;
+        const int j = (e % LBV) * VL;
+        if (i < b.va && j < b.vb) {
 #pragma unroll
-      for (int k = 0; k < VL; ++k) tile[i * PITCH + j + k] = x[r].v[k];
+          for (int k = 0; k < VL; ++k) tile[Slots::at(i, j + k)] = x[r].v[k];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < RS; ++r) {
+        const int e = tid + r * BS;
+        const int j = e / LAV;
+        const int i = (e % LAV) * VS;
+        if (i < b.va && j < b.vb) {
+          Vec<P, VS> y;
+#pragma unroll
+          for (int k = 0; k < VS; ++k) y.v[k] = tile[Slots::at(i + k, j)];
+          nt_store<P, VS>(d + i + tile_dst_b(tp, j), y);
+        }
+      }
+      __syncthreads();  // the next tile is parked over this one
     }
+    return;
   }
-  __syncthreads();
+  unsigned int t = blockIdx.x;
+  if (t >= tiles) return;
+  // Narrow: each slot's offset is kept as an unsigned 32-bit byte offset from
+  // a uniform corner of the tile (the base moved by the in-tile strides'
+  // negative parts), so every access is a scalar base plus a 32-bit lane
+  // offset; otherwise as a 64-bit element offset from the tile's base.
+  using Off = std::conditional_t<Narrow, unsigned int, long long>;
+  long long s_shift = 0, d_shift = 0;
+  if constexpr (Narrow) {
+    auto low = [](long long stride, unsigned int count) {
+      return stride < 0 ? stride * static_cast<long long>(count - 1) : 0ll;
+    };
+    s_shift = low(tp.a_ss0, tp.a_in.d) + low(tp.a_ss1, tp.a_tile);
+    d_shift = low(tp.b_ds0, tp.b_in.d) + low(tp.b_ds1, tp.b_tile);
+  }
+  auto narrow = [](long long elements) {
+    return static_cast<Off>(Narrow ? elements * static_cast<long long>(sizeof(P)) : elements);
+  };
+  Off soff[RL], doff[RS];
+#pragma unroll
+  for (int r = 0; r < RL; ++r) {
+    const int e = tid + r * BS;
+    soff[r] = narrow(tile_src_a(tp, e / LBV) + (e % LBV) * VL - s_shift);
+  }
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
     const int e = tid + r * BS;
-    const int j = e / LAV;
-    const int i = (e % LAV) * VS;
-    if (i < va && j < vb) {
+    doff[r] = narrow((e % LAV) * VS + tile_dst_b(tp, e / LAV) - d_shift);
+  }
+  // The first element of the tile (the load of an empty slot, the store of
+  // an empty slot's stand-in), at offset -shift.
+  const Off s_first = narrow(-s_shift);
+  const Off d_first = narrow(-d_shift);
+  auto at = [](auto* base, long long corner, Off off) {
+    using Q = std::remove_pointer_t<decltype(base)>;
+    if constexpr (Narrow) {
+      using B = std::conditional_t<std::is_const_v<Q>, const char, char>;
+      return reinterpret_cast<Q*>(reinterpret_cast<B*>(base + corner) + off);
+    } else {
+      return base + corner + off;
+    }
+  };
+  Vec<P, VL> x[RL];
+  auto load = [&](const TileBase& b) {
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+      const int e = tid + r * BS;
+      const bool valid = e / LBV < b.va && (e % LBV) * VL < b.vb;
+      x[r] = nt_load<P, VL>(at(src, b.sb + s_shift, valid ? soff[r] : s_first));
+    }
+  };
+  auto park = [&](const TileBase& b) {
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+      const int e = tid + r * BS;
+      const int i = e / LBV;
+      const int j = (e % LBV) * VL;
+      if (i < b.va && j < b.vb) {
+#pragma unroll
+        for (int k = 0; k < VL; ++k) tile[Slots::at(i, j + k)] = x[r].v[k];
+      }
+    }
+  };
+  // Every slot stores: an empty slot of a partial tile stores the tile's
+  // first vector (elements 0 .. VS - 1 of column 0, valid in any non-empty
+  // tile: a partial tile's valid length is a multiple of VS) over itself, the
+  // same bytes its own slot writes. With no branch around them, the compiler
+  // counts exactly RS stores after the next tile's loads and waits for those
+  // loads alone before parking them (a branch would make it wait for the
+  // stores as well).
+  auto store = [&](const TileBase& b) {
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+      const int e = tid + r * BS;
+      const bool valid = e / LAV < b.vb && (e % LAV) * VS < b.va;
+      const int j = valid ? e / LAV : 0;
+      const int i = valid ? (e % LAV) * VS : 0;
       Vec<P, VS> y;
 #pragma unroll
-      for (int k = 0; k < VS; ++k) y.v[k] = tile[(i + k) * PITCH + j];
-      nt_store<P, VS>(d + i + dst_b(j), y);
+      for (int k = 0; k < VS; ++k) y.v[k] = tile[Slots::at(i + k, j)];
+      nt_store<P, VS>(at(dst, b.db + d_shift, valid ? doff[r] : d_first), y);
     }
+  };
+  TileBase cur = tile_base(tp, t);
+  load(cur);
+  park(cur);
+  __syncthreads();
+  for (;;) {
+    // t < tiles, so tiles - t cannot wrap, and neither can t + blocks.
+    if (!(blocks < tiles - t)) {
+      store(cur);
+      return;
+    }
+    t += blocks;
+    const TileBase nb = tile_base(tp, t);
+    load(nb);
+    store(cur);
+    __syncthreads();  // every wave has read the tile before it is overwritten
+    park(nb);
+    __syncthreads();
+    cur = nb;
   }
 }
 
@@ -658,18 +822,18 @@ __device__ __forceinline__ T uniform_copy(const T& shared_value) {
   return out;
 }
 
-// TILED inside the entries: when the plan has a one-tile shape (tile_plan),
-// thread 0 writes the TilePlan into the block's move scratch behind the tile,
-// and the block moves tiles blockIdx.x, blockIdx.x + blocks, ... with the
-// launchers' one-tile body, so a persistent grid plans once per block; other
-// plans and block sizes take the general tile walk, one tile at a time.
+// TILED inside the entries: when the plan has a TilePlan form (tile_plan),
+// thread 0 writes it into the block's move scratch behind the tile, and the
+// block moves tiles blockIdx.x, blockIdx.x + blocks, ... with the launchers'
+// tile body, one tile at a time, so a persistent grid plans once per block;
+// other plans and block sizes take the general tile walk.
 template <typename P>
 __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, const MovePlan& p,
                                                  unsigned char* lds, unsigned int blocks) {
   if constexpr (sizeof(P) >= 4) {
     constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
     constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
-    constexpr int kTileBytes = LA * (LB + 1) * static_cast<int>(sizeof(P));
+    constexpr int kTileBytes = TileSlots<P, LA, LB, 1>::kElems * static_cast<int>(sizeof(P));
     static_assert(kTileBytes + static_cast<int>(sizeof(TilePlan)) <= kMoveLdsBytes,
                   "the tile and its plan share the move scratch");
     if (blockDim.x == static_cast<unsigned>(kBlock)) {
@@ -690,11 +854,8 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
         auto walk = [&](auto vl_tag, auto vs_tag) {
           constexpr int VLt = decltype(vl_tag)::value;
           constexpr int VSt = decltype(vs_tag)::value;
-          for (unsigned int t = blockIdx.x; t < tiles; t += blocks) {
-            move_tile_once<P, VLt, VSt, LA, LB, true>(static_cast<P*>(dst),
-                                                      static_cast<const P*>(src), tp, tile, t);
-            __syncthreads();  // the tile's LDS is rewritten by the next one
-          }
+          move_tile_walk<P, VLt, VSt, LA, LB, TilePlan, false, false>(
+              static_cast<P*>(dst), static_cast<const P*>(src), tp, tile, tiles, blocks);
         };
         using VV = std::integral_constant<int, V>;
         using V1 = std::integral_constant<int, 1>;
@@ -763,8 +924,8 @@ __device__ __forceinline__ void move_entry(void* dst, const void* src, int dtype
                                            long long len) {
   const int es = dtype_size(dtype);
   if (es == 0) return;  // unknown tag: no work (reference c-kernel-abi.md:107-108)
-  if (entry_block_idle()) return;
-  const unsigned int blocks = entry_blocks();
+  if (entry_block_idle(kMoveEntryWaves)) return;
+  const unsigned int blocks = entry_blocks(kMoveEntryWaves);
   __shared__ MovePlan plan;
   __shared__ alignas(16) unsigned char lds[kMoveLdsBytes];
   if (threadIdx.x == 0) move_plan(&plan, src_layout, dst_strides, dst_offset, len, es);
@@ -819,8 +980,8 @@ __device__ __forceinline__ void move_entry_by(void* dst, const void* src, int dt
                                               long long dst_offset, long long len) {
   const int es = dtype_size(dtype);
   if (es == 0 || len <= 0 || !ok || rank < 0) return;
-  if (entry_block_idle()) return;
-  const unsigned int blocks = entry_blocks();
+  if (entry_block_idle(kMoveEntryWaves)) return;
+  const unsigned int blocks = entry_blocks(kMoveEntryWaves);
   __shared__ MovePlan plan;
   __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
   __shared__ int fused;
@@ -998,8 +1159,8 @@ __device__ __forceinline__ void fill_view_entry(void* out, int dtype, int rank, 
                                                 long long len) {
   const int es = dtype_size(dtype);
   if (es == 0 || len <= 0 || rank < 0) return;
-  if (entry_block_idle()) return;
-  const unsigned int blocks = entry_blocks();
+  if (entry_block_idle(kMoveEntryWaves)) return;
+  const unsigned int blocks = entry_blocks(kMoveEntryWaves);
   __shared__ FillPlan plan;
   __shared__ long long fe[kMaxFusedDims], fs[kMaxFusedDims], fd[kMaxFusedDims];
   __shared__ int fused;
@@ -1077,12 +1238,25 @@ __global__ void __launch_bounds__(kBlock)
   move_row_units<P, V, NTL, NR>(dst, src, rp, blocks);
 }
 
-template <typename P, int VL, int VS, int LA, int LB>
-__global__ void __launch_bounds__(kBlock)
-    move_tile_once_kernel(void* dst, const void* src, TilePlan tp) {
-  __shared__ P tile[LA * (LB + 1)];
-  move_tile_once<P, VL, VS, LA, LB>(static_cast<P*>(dst), static_cast<const P*>(src), tp, tile,
-                                    0);
+// Eight wavefronts per SIMD for the narrow walk of 16-byte elements: its
+// scalar registers (102) otherwise hold it to seven, and a grid of seven
+// blocks per CU leaves C5's 16,384 tiles 9.14 rounds, a tenth round in which
+// one block in seven works (97.2 against 100.2 us with the request, which
+// moves 32 scalar registers to vector lanes). The 8-byte walk already has
+// eight (99 scalar registers); the request made it spill 74 and run 3 %
+// slower on C3.
+template <typename P>
+constexpr int walk_waves(bool narrow) {
+  return narrow && sizeof(P) == 16 ? 8 : 1;
+}
+
+template <typename P, int VL, int VS, int LA, int LB, typename TP, bool Narrow>
+__global__ void __launch_bounds__(kBlock, walk_waves<P>(Narrow))
+    move_tile_walk_kernel(void* dst, const void* src, TP tp, unsigned int tiles) {
+  __shared__ P tile[TileSlots<P, LA, LB, VL>::kElems];
+  move_tile_walk<P, VL, VS, LA, LB, TP, Narrow>(static_cast<P*>(dst),
+                                                static_cast<const P*>(src), tp, tile, tiles,
+                                                gridDim.x);
 }
 
 template <typename P, int BS>
@@ -1331,25 +1505,63 @@ bool config_valid(const t4a_cuda_transpose_config& c) {
          T4A_OK;
 }
 
+// Blocks of Kernel (kBlock threads, no dynamic LDS) that the current device
+// holds at once -- its occupancy per CU times the CU count -- queried once
+// per device; kTileWalkBlocks if the runtime cannot say.
+template <auto Kernel>
+unsigned int resident_blocks() {
+  static std::atomic<unsigned int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return t4a::kTileWalkBlocks;
+  unsigned int v = cache[dev].load(std::memory_order_relaxed);
+  if (v != 0) return v;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, t4a::kBlock, 0) !=
+          hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      per_cu <= 0 || cus <= 0)
+    return t4a::kTileWalkBlocks;
+  v = static_cast<unsigned int>(per_cu) * static_cast<unsigned int>(cus);
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// The tile walk's own grid, whatever the caller's geometry (one block per
+// tile) was: as many blocks as the device holds at once (a larger grid would
+// leave its last blocks a whole walk to do after the others finish), at most
+// one per tile.
+template <auto Kernel, typename TP>
+void launch_tile_walk(unsigned int tiles, hipStream_t s, void* dst, const void* src,
+                      const TP& tp) {
+  const unsigned int resident = resident_blocks<Kernel>();
+  hipLaunchKernelGGL(Kernel, dim3(tiles < resident ? tiles : resident), dim3(t4a::kBlock), 0, s,
+                     dst, src, tp, tiles);
+}
+
 template <typename P, int VL, int VS>
-void launch_tile_shape(dim3 grid, hipStream_t s, void* dst, const void* src,
+void launch_tile_shape(unsigned int tiles, hipStream_t s, void* dst, const void* src,
                        const t4a::TilePlan& tp) {
   constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
   constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
-  hipLaunchKernelGGL((t4a::move_tile_once_kernel<P, VL, VS, LA, LB>), grid, dim3(t4a::kBlock), 0,
-                     s, dst, src, tp);
+  if (tp.ncoord <= t4a::kCompactCoords &&
+      t4a::tile_offsets_narrow(tp, LA, LB, static_cast<int>(sizeof(P))))
+    launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>>(
+        tiles, s, dst, src, t4a::compact_tile_plan(tp));
+  else
+    launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlan, false>>(
+        tiles, s, dst, src, tp);
 }
 
 // The one-tile kernels by vector widths (t4a::tile_once_shape's shapes).
 template <typename P, int V>
-void launch_tile_once(bool vl, bool vs, dim3 grid, hipStream_t s, void* dst, const void* src,
-                      const t4a::TilePlan& tp) {
+void launch_tile_once(bool vl, bool vs, unsigned int tiles, hipStream_t s, void* dst,
+                      const void* src, const t4a::TilePlan& tp) {
   if constexpr (V > 1) {
-    if (vl && vs) return launch_tile_shape<P, V, V>(grid, s, dst, src, tp);
-    if (vl) return launch_tile_shape<P, V, 1>(grid, s, dst, src, tp);
-    if (vs) return launch_tile_shape<P, 1, V>(grid, s, dst, src, tp);
+    if (vl && vs) return launch_tile_shape<P, V, V>(tiles, s, dst, src, tp);
+    if (vl) return launch_tile_shape<P, V, 1>(tiles, s, dst, src, tp);
+    if (vs) return launch_tile_shape<P, 1, V>(tiles, s, dst, src, tp);
   }
-  launch_tile_shape<P, 1, 1>(grid, s, dst, src, tp);
+  launch_tile_shape<P, 1, 1>(tiles, s, dst, src, tp);
 }
 
 // A compact 2-D transpose found in a movement plan, on the tiled transpose's
@@ -1450,7 +1662,7 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
       if (block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 && block.z == 1 &&
           grid.y == 1 && grid.z == 1 && static_cast<long long>(grid.x) == plan.tiles &&
           t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P)))) {
-        launch_tile_once<P, V>(vl, vs, grid, s, dst, src, tp);
+        launch_tile_once<P, V>(vl, vs, grid.x, s, dst, src, tp);
         return status_of_last_launch();
       }
     }

@@ -168,9 +168,10 @@ void movement_launch(const t4a::MovePlan& plan, int esize, t4a_launch* out) {
   long long blocks = 0;
   t4a::TilePlan tp;
   switch (plan.mode) {
-    // A tile shape of the one-tile kernels: one block per tile. Otherwise
-    // tiled blocks are persistent: four per CU on 256 CUs, each pipelining its
-    // run of tiles (the next tile's loads overlap the current tile's stores).
+    // A TilePlan shape: one block per tile (the launchers then walk the
+    // tiles with a persistent grid of their own). Otherwise tiled blocks are
+    // persistent: four per CU on 256 CUs, each pipelining its run of tiles
+    // (the next tile's loads overlap the current tile's stores).
     case t4a::kMoveTiled:
       blocks = t4a::tile_plan(&tp, plan, esize) ? plan.tiles
                                                   : (plan.tiles < 1024 ? plan.tiles : 1024);

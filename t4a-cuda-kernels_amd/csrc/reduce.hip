@@ -295,6 +295,47 @@ __device__ __forceinline__ void decode_output(const UnitPlan& up, long long o, l
   unit_decode(up, static_cast<unsigned int>(o), ib, ob);
 }
 
+// UNIT over a one-group axis on a compact plan (kBlock threads a block): runs
+// of 64 * U consecutive outputs a wavefront, lane l the outputs run + l + 64u
+// (unit_outputs_grouped's walk with 32-bit indices; `blocks`, the grid's block
+// count, is needed only past the first run).
+template <typename Fold, typename T>
+__device__ __forceinline__ void unit_group_lean(T* __restrict__ out, const T* __restrict__ in,
+                                                const UnitPlan& up, unsigned int output_len,
+                                                Fold f, unsigned int blocks) {
+  constexpr int V = VecLanes<T>::value;
+  constexpr int U = kUnitOutputsPerThread;
+  constexpr unsigned int kRun = kWave * U;
+  const int len = up.axis_len;
+  const unsigned int lane = threadIdx.x % kWave;
+  const unsigned int wave = (blockIdx.x * kBlock + threadIdx.x) / kWave;
+  for (unsigned int run = wave * kRun; run < output_len;
+       run += blocks * (kBlock / kWave) * kRun) {
+    Group<T, V> g[U];
+    long long ob[U];
+    const T* xs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const unsigned int o = run + lane + kWave * u;
+      long long ib;
+      unit_decode(up, o < output_len ? o : run, &ib, &ob[u]);
+      xs[u] = in + ib;
+      const Vec<T, V> x = nt_load<T, V>(xs[u]);
+      __builtin_memcpy(&g[u], &x, sizeof(g[u]));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (run + lane + kWave * u < output_len) {
+        T acc = f.seed(g[u].x[0]);
+#pragma unroll
+        for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
+        for (int i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
+        nt_store<T, 1>(out + ob[u], Vec<T, 1>{{acc}});
+      }
+    }
+  }
+}
+
 template <typename Fold, typename T, int BS>
 __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restrict__ in,
                                           const UnitPlan& up, unsigned int output_len, Fold f) {
@@ -305,38 +346,7 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
     if (up.vector) {
       if constexpr (BS == kBlock) {
         if (len < 2 * V) {
-          // One group per output: runs of 64 * U consecutive outputs a
-          // wavefront, lane l the outputs run + l + 64u (unit_outputs_grouped's
-          // walk with 32-bit indices).
-          constexpr int U = kUnitOutputsPerThread;
-          constexpr unsigned int kRun = kWave * U;
-          const unsigned int lane = threadIdx.x % kWave;
-          const unsigned int wave = (blockIdx.x * BS + threadIdx.x) / kWave;
-          const unsigned int run_stride = gstride / kWave * kRun;
-          for (unsigned int run = wave * kRun; run < output_len; run += run_stride) {
-            Group<T, V> g[U];
-            long long ob[U];
-            const T* xs[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-              const unsigned int o = run + lane + kWave * u;
-              long long ib;
-              unit_decode(up, o < output_len ? o : run, &ib, &ob[u]);
-              xs[u] = in + ib;
-              const Vec<T, V> x = nt_load<T, V>(xs[u]);
-              __builtin_memcpy(&g[u], &x, sizeof(g[u]));
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-              if (run + lane + kWave * u < output_len) {
-                T acc = f.seed(g[u].x[0]);
-#pragma unroll
-                for (int c = 1; c < V; ++c) acc = f.fold(acc, g[u].x[c]);
-                for (int i = V; i < len; ++i) acc = f.fold(acc, xs[u][i]);
-                nt_store<T, 1>(out + ob[u], Vec<T, 1>{{acc}});
-              }
-            }
-          }
+          unit_group_lean<Fold, T>(out, in, up, output_len, f, gridDim.x);
           return;
         }
       }
@@ -1367,6 +1377,18 @@ __global__ void __launch_bounds__(BS)
                          Fold{});
 }
 
+// UNIT over a one-group axis (C4's i32 product), a kernel of its own: its
+// wavefronts live for two loads, and in the kernel that carries every unit
+// walk the prologue computed the other walks' invariants (and spilled scalar
+// registers) before the first load. The block count is an argument.
+template <typename T, typename Fold>
+__global__ void __launch_bounds__(kBlock)
+    reduce_unit_group_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len,
+                             unsigned int blocks) {
+  unit_group_lean<Fold, T>(static_cast<T*>(out), static_cast<const T*>(in), up, output_len,
+                           Fold{}, blocks);
+}
+
 // PLANE on a compact plan (the combine over thousands of partials): the plane
 // body with the UnitPlan decode and the fold fixed at compile time. The general
 // kernel's by-value eight-dim geometry takes a private segment, which every
@@ -1469,8 +1491,8 @@ extern "C" __global__ void __launch_bounds__(512)
     t4a_cuda_reduce(void* out, const void* in, int dtype, int op, int strategy,
                     t4a_cuda_layout out_layout, t4a_cuda_layout in_layout, int axis,
                     long long output_len) {
-  if (t4a::entry_block_idle()) return;
-  const unsigned int blocks = t4a::entry_blocks();
+  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
   __shared__ t4a::ReduceDims rd;
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
   if (threadIdx.x == 0) t4a::reduce_dims(&rd, out_layout, in_layout, axis);
@@ -1487,8 +1509,8 @@ extern "C" __global__ void __launch_bounds__(256)
                              t4a_cuda_layout partials_layout, t4a_cuda_layout in_layout,
                              int axis, long long output_len, long long splits,
                              long long chunk_len) {
-  if (t4a::entry_block_idle()) return;
-  const unsigned int blocks = t4a::entry_blocks();
+  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
   __shared__ t4a::PartialsPlan pp;
   if (threadIdx.x == 0) {
     const int w = blockDim.x <= 32u ? static_cast<int>(blockDim.x) : t4a::kWarp;
@@ -1525,8 +1547,8 @@ extern "C" __global__ void __launch_bounds__(512)
     t4a_cuda_reduce_any(void* out, const void* in, int dtype, int op, int strategy,
                         t4a_cuda_layout_any out_layout, t4a_cuda_layout_any in_layout, int axis,
                         long long output_len) {
-  if (t4a::entry_block_idle()) return;
-  const unsigned int blocks = t4a::entry_blocks();
+  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
   __shared__ t4a::ReduceDimsWide rd;
   __shared__ alignas(16) unsigned char warp_lds[16 * sizeof(t4a::c64)];
   if (threadIdx.x == 0) any_dims(&rd, out_layout, in_layout, axis);
@@ -1588,8 +1610,8 @@ extern "C" __global__ void __launch_bounds__(256)
   __shared__ int side_cpl;
   __shared__ alignas(16) unsigned char tiles_lds[(t4a::kBlock / t4a::kWave) * t4a::kWave * 2 * 8];
   __shared__ int redo;
-  if (t4a::entry_block_idle()) return;
-  const unsigned int blocks = t4a::entry_blocks();
+  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
   const bool whole_waves = blockDim.x == static_cast<unsigned>(t4a::kBlock) &&
                            blockDim.y == 1 && blockDim.z == 1;
   if (threadIdx.x == 0) {
@@ -1660,6 +1682,14 @@ namespace {
 template <typename T, typename Fold>
 void launch_unit_fold(unsigned threads, dim3 grid, dim3 block, hipStream_t s, void* out,
                       const void* in, const t4a::UnitPlan& up, unsigned int output_len) {
+  if constexpr (t4a::VecLanes<T>::value > 0) {
+    if (threads == static_cast<unsigned>(t4a::kBlock) && up.vector &&
+        up.axis_len < 2 * t4a::VecLanes<T>::value) {
+      hipLaunchKernelGGL((t4a::reduce_unit_group_kernel<T, Fold>), grid, block, 0, s, out, in,
+                         up, output_len, grid.x);
+      return;
+    }
+  }
   if (threads == static_cast<unsigned>(t4a::kBlock))
     hipLaunchKernelGGL((t4a::reduce_unit_lean_kernel<T, Fold, t4a::kBlock>), grid, block, 0, s,
                        out, in, up, output_len);
