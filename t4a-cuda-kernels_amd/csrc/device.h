@@ -64,6 +64,17 @@ __device__ __forceinline__ unsigned int entry_blocks(unsigned int waves) {
   return gridDim.x < cap ? gridDim.x : cap;
 }
 
+// The pass-1 entries: blocks of one wavefront or less (the reference
+// geometry's one-plane blocks, 262,144 of them for C2) keep 2048 working
+// blocks, so that the returning blocks still find slots (and each working
+// plane keeps several cubes in flight); larger blocks keep 8192 wavefronts'
+// worth, as the other reduction entries do. C2's f32 sums under the reference
+// geometry (both passes) took 106-111 us with 2048, 113-116 with 4096,
+// 118-128 with 8192 and 118-137 with 1024.
+__device__ __forceinline__ unsigned int partials_entry_waves() {
+  return blockDim.x * blockDim.y * blockDim.z <= 64u ? 2048u : kReduceEntryWaves;
+}
+
 __device__ __forceinline__ bool entry_block_idle(unsigned int waves) {
   return blockIdx.y != 0 || blockIdx.z != 0 || blockIdx.x >= entry_blocks(waves);
 }

@@ -646,7 +646,7 @@ using TilePlanCompact = TilePlanN<kCompactCoords>;
 // Whether the in-tile offsets of the valid slots -- the source offset of row
 // i plus a column, the destination offset of column j plus a row, for an LA x
 // LB tile of esize-byte elements -- span fewer than 2^31 bytes on each side.
-inline bool tile_offsets_narrow(const TilePlan& tp, int la, int lb, int esize) {
+T4A_HD bool tile_offsets_narrow(const TilePlan& tp, int la, int lb, int esize) {
   auto mag = [](long long v) { return v < 0 ? -static_cast<double>(v) : static_cast<double>(v); };
   const double src = mag(tp.a_ss0) * (tp.a_in.d - 1.0) + mag(tp.a_ss1) * (tp.a_tile - 1.0) + lb;
   const double dst = mag(tp.b_ds0) * (tp.b_in.d - 1.0) + mag(tp.b_ds1) * (tp.b_tile - 1.0) + la;
@@ -1159,8 +1159,12 @@ struct SidePlan {
   long long units;
 };
 
-T4A_HD SidePlan side_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
-  SidePlan sp;
+// Written through a pointer: a kernel's thread 0 builds it in LDS, where the
+// runtime-subscripted writes below need no per-lane scratch memory (a local
+// SidePlan would).
+T4A_HD void side_plan_into(SidePlan* out, const PartialsPlan& p, long long splits,
+                           long long chunk_len) {
+  SidePlan& sp = *out;
   const ReduceDims& d = p.dims;
   sp.in_offset = d.in_offset;
   sp.out_offset = d.out_offset;
@@ -1186,6 +1190,11 @@ T4A_HD SidePlan side_plan(const PartialsPlan& p, long long splits, long long chu
   sp.last_len = static_cast<int>(d.axis_len - (splits - 1) * chunk_len);
   sp.columns = p.columns;
   sp.units = p.units;
+}
+
+T4A_HD SidePlan side_plan(const PartialsPlan& p, long long splits, long long chunk_len) {
+  SidePlan sp;
+  side_plan_into(&sp, p, splits, chunk_len);
   return sp;
 }
 

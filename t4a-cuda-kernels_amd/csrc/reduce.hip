@@ -846,6 +846,79 @@ __device__ __forceinline__ void partials_lean(void* partials_ptr, const void* in
   }
 }
 
+// Cube `cube` of a LeanPlan: its chunk, its partial's offset and its length
+// (cube = o * splits + split, o over the fused dims, first dim fastest).
+template <typename T>
+__device__ __forceinline__ void lean_cube(const LeanPlan& lp, const T* in, unsigned int cube,
+                                          const T** chunk, long long* pidx, int* len) {
+  unsigned int o = div_by(cube, lp.splits);
+  const unsigned int split = cube - o * lp.splits.d;
+  long long ib = lp.in_offset;
+  long long pb = lp.out_offset;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (k < lp.n) {
+      unsigned int c = o;
+      if (k + 1 < lp.n) {
+        const unsigned int q = div_by(o, lp.ext[k]);
+        c = o - q * lp.ext[k].d;
+        o = q;
+      }
+      ib += static_cast<long long>(c) * lp.is[k];
+      pb += static_cast<long long>(c) * lp.os[k];
+    }
+  }
+  *chunk = in + ib + static_cast<long long>(split) * lp.chunk_len;
+  *pidx = pb + static_cast<long long>(split) * lp.out_axis_stride;
+  *len = split + 1 == lp.splits.d ? lp.last_len : static_cast<int>(lp.chunk_len);
+}
+
+// LEAN inside the reduce_partials entry, for the caller's block shape: a
+// block of 32-lane planes (blockDim.x / 32 of them), the working blocks'
+// planes striding over the cubes. Under the reference's geometry a block is
+// often one 32-lane plane, and few blocks work (the rest return): each plane
+// issues the loads of C cubes before it folds the first, so that it keeps
+// C chunks in flight instead of one. Each cube folds as partials_lean folds it.
+template <typename Fold, typename T, int K, int C>
+__device__ __forceinline__ void partials_lean_entry(void* partials_ptr, const void* in_ptr,
+                                                    const LeanPlan& lp, Fold f,
+                                                    unsigned int blocks) {
+  constexpr int W = kWarp;
+  T* partials = static_cast<T*>(partials_ptr);
+  const T* in = static_cast<const T*>(in_ptr);
+  const unsigned int planes = blockDim.x / W;
+  const int lane = threadIdx.x % W;
+  const unsigned int stride = blocks * planes;
+  const unsigned int cubes = lp.cubes;
+  // Below 2^31 cubes (the lean plan's bound) and at most 2^24 planes, base +
+  // C * stride stays below 2^32.
+  for (unsigned int base = blockIdx.x * planes + threadIdx.x / W; base < cubes;
+       base += C * stride) {
+    LeanShare<T, K> sh[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const unsigned int cube = base + c * stride < cubes ? base + c * stride : base;
+      const T* chunk;
+      long long pidx;
+      int len;
+      lean_cube(lp, in, cube, &chunk, &pidx, &len);
+      lean_load<T, K, true>(sh[c], chunk, len, lane);
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const unsigned int cube = base + c * stride;
+      if (cube < cubes) {
+        const T* chunk;
+        long long pidx;
+        int len;
+        lean_cube(lp, in, cube, &chunk, &pidx, &len);
+        const T reduced = lean_fold<Fold, T, K, true>(sh[c], chunk, len, lane, f);
+        if (lane == 0) partials[pidx] = reduced;
+      }
+    }
+  }
+}
+
 // Where a joined reduction writes its finals: output o at offset + o * stride
 // of `out`; each block holds `outputs` whole outputs (their splits' chunks).
 struct JoinedOut {
@@ -931,6 +1004,10 @@ __device__ __forceinline__ void partials_planes_dims(void* partials_ptr, const v
   const bool split_major = rd.axis_stride != 1;
   for (long long idx = static_cast<long long>(blockIdx.x) * planes + threadIdx.x / w;
        idx < cubes; idx += static_cast<long long>(blocks) * planes) {
+    // In the entries the dims live in LDS: without this, their loads are
+    // hoisted out of the loop and held in vector registers for all of it
+    // (about 50 of them, enough to cost the entry kernel an occupancy step).
+    asm volatile("" ::: "memory");
     long long o, split;
     if (split_major) {
       split = idx / output_len;
@@ -1069,28 +1146,31 @@ __device__ __forceinline__ void side_unit(const SidePlan& sp, unsigned int u,
   *len = split + 1 == sp.splits.d ? sp.last_len : sp.chunk_len;
 }
 
-// TILES: a block of four wavefronts per unit (column block, split, other).
-// Lane t holds columns col0 .. col0 + CPL - 1 and wavefront w the plane lanes
-// l = 8w .. 8w + 7 of those columns' cubes; plane lane l folds rows
-// start + l + 32k in k order. A wavefront joins its eight plane lanes with the
-// pairwise tree as they finish (a binary counter over l), and the four subtree
-// values meet through LDS as ((w0 + w1) + (w2 + w3)): together, the plane's
-// own-left xor tree.
-template <typename Fold, typename T, int CPL>
+// TILES: a block of NW wavefronts of WL lanes per unit (column block, split,
+// other): four of 64 in the launchers; one, two or four in the entries, whose
+// geometry the caller sets (one wavefront of 32 lanes for the reference's
+// 32-thread blocks). Lane t holds columns col0 .. col0 + CPL - 1 and wavefront
+// w the plane lanes l = (32 / NW) w .. (32 / NW)(w + 1) - 1 of those columns'
+// cubes; plane lane l folds rows start + l + 32k in k order. A wavefront joins
+// its plane lanes with the pairwise tree as they finish (a binary counter over
+// l), and the NW subtree values meet through LDS as ((w0 + w1) + (w2 + w3)):
+// together, the plane's own-left xor tree.
+template <typename Fold, typename T, int CPL, int NW = kBlock / kWave, int WL = kWave>
 __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* in_ptr,
                                                const SidePlan& sp, Fold f, T* lds, int* redo,
                                                unsigned int blocks) {
-  constexpr int kWaves = kBlock / kWave;
-  constexpr int kLanesPerWave = kWarp / kWaves;  // plane lanes per wavefront: 8
-  constexpr int BC = kWave * CPL;                // columns per block
-  static_assert(kLanesPerWave == 8, "the streaming tree below is written for 8 lanes");
+  static_assert(NW == 1 || NW == 2 || NW == 4, "one, two or four wavefronts");
+  static_assert(WL == kWave || (WL == kWarp && NW == 1), "64-lane wavefronts or one of 32");
+  constexpr int kLanesPerWave = kWarp / NW;  // plane lanes per wavefront: 32, 16 or 8
+  constexpr int kLevels = NW == 1 ? 5 : NW == 2 ? 4 : 3;
+  constexpr int BC = WL * CPL;  // columns per block
   T* partials = static_cast<T*>(partials_ptr);
   const char* in = static_cast<const char*>(in_ptr);
   // The wavefront index, explicitly uniform: the compiler cannot tell that
   // threadIdx.x / 64 is, and would otherwise turn every row test below into a
   // divergent branch.
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int t = threadIdx.x % kWave;
+  const int w = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int t = threadIdx.x % WL;
   const long long row_bytes = sp.axis_stride * static_cast<long long>(sizeof(T));
   const long long lane_off = static_cast<long long>(t) * CPL * static_cast<long long>(sizeof(T));
   for (long long u = blockIdx.x; u < sp.units; u += blocks) {
@@ -1102,10 +1182,10 @@ __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* i
     const bool active = block_col + t * CPL < sp.columns;  // CPL divides the column count
     // the block's first column at row 0 of the split, uniform across the block
     const char* rows = in + (ib + block_col) * static_cast<long long>(sizeof(T));
-    // One pass of the unit under fold g: each wavefront's 8-lane subtree into
-    // LDS, then wavefront 0's columns meet as ((w0+w1)+(w2+w3)) in r.
+    // One pass of the unit under fold g: each wavefront's subtree (into LDS
+    // when there are several), then wavefront 0's columns meet in r.
     auto pass = [&](auto g, T* r) {
-      T level[3][CPL];
+      T level[kLevels][CPL];
       T sub[CPL];
       // Two plane lanes per step keep two lanes' loads in flight; the tree's
       // climb is a uniform branch on the lane index.
@@ -1120,38 +1200,44 @@ __device__ __forceinline__ void partials_tiles(void* partials_ptr, const void* i
 #pragma unroll
           for (int c = 0; c < CPL; ++c) acc[c] = T{};
         }
-        // Binary counter: lane a's value climbs while a ends in ones.
-        if ((a & 1) == 0) {
+        // Binary counter: lane a's value climbs while a ends in ones; the
+        // last lane (all ones) carries the wavefront's whole subtree.
+        bool parked = false;
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) level[0][c] = acc[c];
-        } else {
+        for (int lv = 0; lv < kLevels; ++lv) {
+          if (!parked) {
+            if (((a >> lv) & 1) == 0) {
 #pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = g.combine(level[0][c], acc[c]);
-          if ((a & 2) == 0) {
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) level[1][c] = acc[c];
-          } else {
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) acc[c] = g.combine(level[1][c], acc[c]);
-            if ((a & 4) == 0) {
-#pragma unroll
-              for (int c = 0; c < CPL; ++c) level[2][c] = acc[c];
+              for (int c = 0; c < CPL; ++c) level[lv][c] = acc[c];
+              parked = true;
             } else {
 #pragma unroll
-              for (int c = 0; c < CPL; ++c) sub[c] = g.combine(level[2][c], acc[c]);
+              for (int c = 0; c < CPL; ++c) acc[c] = g.combine(level[lv][c], acc[c]);
             }
           }
         }
+        if (!parked) {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) sub[c] = acc[c];
+        }
       }
+      if constexpr (NW == 1) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) lds[w * BC + t * CPL + c] = sub[c];
-      __syncthreads();
-      if (w == 0 && active) {
+        for (int c = 0; c < CPL; ++c) r[c] = sub[c];
+      } else {
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int i = t * CPL + c;
-          r[c] = g.combine(g.combine(lds[i], lds[BC + i]),
-                           g.combine(lds[2 * BC + i], lds[3 * BC + i]));
+        for (int c = 0; c < CPL; ++c) lds[w * BC + t * CPL + c] = sub[c];
+        __syncthreads();
+        if (w == 0 && active) {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) {
+            const int i = t * CPL + c;
+            if constexpr (NW == 2)
+              r[c] = g.combine(lds[i], lds[BC + i]);
+            else
+              r[c] = g.combine(g.combine(lds[i], lds[BC + i]),
+                               g.combine(lds[2 * BC + i], lds[3 * BC + i]));
+          }
         }
       }
     };
@@ -1504,25 +1590,99 @@ extern "C" __global__ void __launch_bounds__(512)
   });
 }
 
+// Pass 1 under the caller's geometry: thread 0 plans as the launchers do for
+// this block shape. A strided axis with neighbouring output columns takes the
+// TILES mapping when the block is one to four whole wavefronts or one 32-lane
+// plane (the reference's shapes); a contiguous axis whose chunks fit the LEAN
+// mapping takes it with the block's planes; anything else walks planes.
 extern "C" __global__ void __launch_bounds__(256)
     t4a_cuda_reduce_partials(void* partials, const void* in, int dtype, int op,
                              t4a_cuda_layout partials_layout, t4a_cuda_layout in_layout,
                              int axis, long long output_len, long long splits,
                              long long chunk_len) {
-  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
-  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
+  if (t4a::entry_block_idle(t4a::partials_entry_waves())) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::partials_entry_waves());
   __shared__ t4a::PartialsPlan pp;
+  __shared__ t4a::SidePlan side;
+  __shared__ t4a::LeanPlan lean;
+  // 0: planes; 1 or 2: TILES with that many columns per lane; -K: LEAN, K slots
+  __shared__ int route;
+  __shared__ alignas(16) unsigned char tiles_lds[t4a::kBlock * 2 * 8];
+  __shared__ int redo;
+  const unsigned int bs = blockDim.x;
+  const bool flat = blockDim.y == 1 && blockDim.z == 1;
   if (threadIdx.x == 0) {
-    const int w = blockDim.x <= 32u ? static_cast<int>(blockDim.x) : t4a::kWarp;
-    t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, w, 0,
-                       t4a::dtype_size(dtype), 1);
+    const int w = bs <= 32u ? static_cast<int>(bs) : t4a::kWarp;
+    const bool tile_shape = flat && (bs == 32 || bs == 64 || bs == 128 || bs == 256);
+    const uintptr_t address = reinterpret_cast<uintptr_t>(in);
+    const int align =
+        (address & 15) == 0 ? 16 : (address & 7) == 0 ? 8 : (address & 3) == 0 ? 4 : 1;
+    t4a::partials_plan(&pp, partials_layout, in_layout, axis, output_len, splits, w,
+                       tile_shape && t4a::sideways_dtype(dtype) ? 1 : 0, t4a::dtype_size(dtype),
+                       align);
+    route = 0;
+    if (pp.mode == t4a::kPartialsTiles) {
+      // The launchers' plan counts 64-lane column blocks; a 32-lane block
+      // covers half as many columns.
+      const long long bc = static_cast<long long>(bs == 32 ? t4a::kWarp : t4a::kWave) * pp.cpl;
+      const long long col_blocks = (pp.columns + bc - 1) / bc;
+      const long long units = col_blocks * pp.others * splits;
+      if (units < (1ll << 31)) {
+        t4a::side_plan_into(&side, pp, splits, chunk_len);
+        side.col_blocks = t4a::fast_div(static_cast<unsigned int>(col_blocks));
+        side.units = units;
+        route = pp.cpl;
+      }
+    } else if (pp.mode == t4a::kPartialsPlane && flat && bs % 32 == 0 && align == 16 &&
+               static_cast<unsigned long long>(blocks) * (bs / 32) <= (1ull << 24)) {
+      const int k = t4a::lean_slots(pp, dtype, op, splits, chunk_len, w);
+      if (k > 0) {
+        lean = t4a::lean_plan(pp, splits, chunk_len);
+        route = -k;
+      }
+    }
   }
   __syncthreads();
+  const int r = route;
   t4a::dispatch_dtype(dtype, [&](auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
     t4a::dispatch_fold<T>(op, [&](auto fold) {
-      t4a::partials_planes<decltype(fold), T>(partials, in, pp, output_len, splits, chunk_len,
-                                              fold, blocks);
+      using F = decltype(fold);
+      if constexpr (t4a::VecLanes<T>::value > 0) {
+        if (r > 0) {
+          // From LDS: copied to scalar registers the plan would spill.
+          const t4a::SidePlan& sp = side;
+          T* lds = reinterpret_cast<T*>(tiles_lds);
+          auto tiles = [&](auto cpl_tag) {
+            constexpr int CPL = decltype(cpl_tag)::value;
+            if (bs == 32)
+              t4a::partials_tiles<F, T, CPL, 1, t4a::kWarp>(partials, in, sp, fold, lds, &redo,
+                                                            blocks);
+            else if (bs == 64)
+              t4a::partials_tiles<F, T, CPL, 1>(partials, in, sp, fold, lds, &redo, blocks);
+            else if (bs == 128)
+              t4a::partials_tiles<F, T, CPL, 2>(partials, in, sp, fold, lds, &redo, blocks);
+            else
+              t4a::partials_tiles<F, T, CPL, 4>(partials, in, sp, fold, lds, &redo, blocks);
+          };
+          if (r == 2)
+            tiles(std::integral_constant<int, 2>{});
+          else
+            tiles(std::integral_constant<int, 1>{});
+          return;
+        }
+        if (r < 0) {
+          const t4a::LeanPlan& lp = lean;
+          switch (-r) {
+            case 1: t4a::partials_lean_entry<F, T, 1, 4>(partials, in, lp, fold, blocks); break;
+            case 2: t4a::partials_lean_entry<F, T, 2, 4>(partials, in, lp, fold, blocks); break;
+            case 3: t4a::partials_lean_entry<F, T, 3, 2>(partials, in, lp, fold, blocks); break;
+            default: t4a::partials_lean_entry<F, T, 4, 2>(partials, in, lp, fold, blocks); break;
+          }
+          return;
+        }
+      }
+      t4a::partials_planes<F, T>(partials, in, pp, output_len, splits, chunk_len, fold, blocks);
     });
   });
 }
@@ -1595,7 +1755,7 @@ __device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, AnySideScratch
   t4a::partials_plan(&tmp->pp, tmp->p8, tmp->i8, axis8, output_len, splits, t4a::kWarp, 1,
                      t4a::dtype_size(dtype), align);
   if (tmp->pp.mode != t4a::kPartialsTiles) return 0;
-  *side = t4a::side_plan(tmp->pp, splits, chunk_len);
+  t4a::side_plan_into(side, tmp->pp, splits, chunk_len);
   return tmp->pp.cpl;
 }
 
@@ -1610,8 +1770,8 @@ extern "C" __global__ void __launch_bounds__(256)
   __shared__ int side_cpl;
   __shared__ alignas(16) unsigned char tiles_lds[(t4a::kBlock / t4a::kWave) * t4a::kWave * 2 * 8];
   __shared__ int redo;
-  if (t4a::entry_block_idle(t4a::kReduceEntryWaves)) return;
-  const unsigned int blocks = t4a::entry_blocks(t4a::kReduceEntryWaves);
+  if (t4a::entry_block_idle(t4a::partials_entry_waves())) return;
+  const unsigned int blocks = t4a::entry_blocks(t4a::partials_entry_waves());
   const bool whole_waves = blockDim.x == static_cast<unsigned>(t4a::kBlock) &&
                            blockDim.y == 1 && blockDim.z == 1;
   if (threadIdx.x == 0) {

@@ -332,3 +332,50 @@ def test_module_reduce_partials(modules, dtype):
                     got = to_host(d_part, want.nbytes)
                     assert np.array_equal(got, want.view(np.uint8)), (extents, axis, op, width,
                                                                       who)
+
+
+# Pass-1 shapes that take the entry's column and lean mappings under both
+# geometries: a strided axis with 8192 / 256 / 96 neighbouring columns (the
+# reference's one-plane 32-thread blocks, its four-plane 128-thread blocks, and
+# ours), and a contiguous axis in 256-element chunks (lean, one and four planes
+# per block), with a 4-byte-misaligned input (no lean, no paired columns) and a
+# partial last column block.
+ROUTE_SHAPES = [([8192, 700], 1, 0), ([256, 2000], 1, 0), ([96, 3000], 1, 0),
+                ([8192, 512], 0, 0), ([8192, 64], 0, 0), ([8192, 600], 1, 1),
+                ([8192, 512], 0, 1), ([200, 900], 1, 0)]
+
+
+@pytest.mark.parametrize("dtype", REAL, ids=[d.name for d in REAL])
+def test_module_reduce_partials_routes(modules, dtype):
+    rng = np.random.default_rng(36)
+    es = dtype.size
+    for extents, axis, lead in ROUTE_SHAPES:
+        n = int(np.prod(extents))
+        x = reduce_inputs(dtype, n + lead, rng)
+        d_in = to_device(x)
+        in_l = t.Layout(list(extents), t.Layout.compact(extents).strides, lead)
+        oe = list(extents)
+        oe[axis] = 1
+        on = t.Layout.compact(oe).element_count()
+        split = t.split_policy(extents[axis], 32)
+        assert split is not None, extents
+        pl = t.reduction_partials_layout(in_l, axis, split.splits)
+        for op in OPS:
+            if not supported(dtype, op):
+                continue
+            want = np.zeros(pl.element_count(), dtype=NUMPY[dtype])
+            orc.reduce_partials(want, x, dtype, op, 32, pl, in_l, axis, on, split.splits,
+                                split.chunk_len)
+            plan = t.plan_reduce_partials(dtype, op, pl, pl.element_count(), in_l, n + lead,
+                                          axis, split, 32)
+            for who, geo in (("reference", ref_partials(on * split.splits, split.chunk_len, 32)),
+                             ("ours", ours(plan))):
+                say("module reduce_partials route", dtype.name, op.name, extents, axis, lead,
+                    split.splits, split.chunk_len, who, geo)
+                d_part = sentinel(want.nbytes)
+                modules["reduce"].launch(
+                    "t4a_cuda_reduce_partials", *geo, None,
+                    [ptr(d_part), ptr(d_in), c_int(dtype), c_int(op), pl.c, in_l.c,
+                     c_int(axis), c_ll(on), c_ll(split.splits), c_ll(split.chunk_len)])
+                got = to_host(d_part, want.nbytes)
+                assert np.array_equal(got, want.view(np.uint8)), (extents, axis, lead, op, who)
