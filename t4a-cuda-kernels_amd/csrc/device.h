@@ -57,9 +57,18 @@ constexpr unsigned int kReduceEntryWaves = 8192;
 // threads) when the runtime cannot be asked.
 constexpr unsigned int kTileWalkBlocks = 2048;
 
+// A grid of at most this many wavefronts (four of the entry kernels' blocks
+// of 256 threads per CU, what their registers and LDS let the chip hold) has
+// no block waiting for a slot: every block of its first row works, whatever
+// the cap. This build's planner gives the entries such grids where it can
+// (TILED plans); the reference's per-element grids are far larger.
+constexpr unsigned int kEntryResidentWaves = 4096;
+
 __device__ __forceinline__ unsigned int entry_blocks(unsigned int waves) {
   const unsigned int waves_per_block = (blockDim.x * blockDim.y * blockDim.z + 63u) / 64u;
-  unsigned int cap = waves / (waves_per_block ? waves_per_block : 1u);
+  const unsigned int wpb = waves_per_block ? waves_per_block : 1u;
+  if (static_cast<unsigned long long>(gridDim.x) * wpb <= kEntryResidentWaves) return gridDim.x;
+  unsigned int cap = waves / wpb;
   if (cap == 0) cap = 1;
   return gridDim.x < cap ? gridDim.x : cap;
 }

@@ -1660,9 +1660,8 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
     if constexpr (sizeof(P) >= 4) {
       t4a::TilePlan tp;
       if (block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 && block.z == 1 &&
-          grid.y == 1 && grid.z == 1 && static_cast<long long>(grid.x) == plan.tiles &&
-          t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P)))) {
-        launch_tile_once<P, V>(vl, vs, grid.x, s, dst, src, tp);
+          grid.y == 1 && grid.z == 1 && t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P)))) {
+        launch_tile_once<P, V>(vl, vs, static_cast<unsigned int>(plan.tiles), s, dst, src, tp);
         return status_of_last_launch();
       }
     }

@@ -166,15 +166,12 @@ int flat_launch_check(long long len) {
 
 void movement_launch(const t4a::MovePlan& plan, int esize, t4a_launch* out) {
   long long blocks = 0;
-  t4a::TilePlan tp;
   switch (plan.mode) {
-    // A TilePlan shape: one block per tile (the launchers then walk the
-    // tiles with a persistent grid of their own). Otherwise tiled blocks are
-    // persistent: four per CU on 256 CUs, each pipelining its run of tiles
-    // (the next tile's loads overlap the current tile's stores).
+    // Tiled blocks are persistent: four per CU on 256 CUs, each walking its
+    // run of tiles (the launchers walk TilePlan shapes with a grid of their
+    // own; this one is what the entries run under, every block working).
     case t4a::kMoveTiled:
-      blocks = t4a::tile_plan(&tp, plan, esize) ? plan.tiles
-                                                  : (plan.tiles < 1024 ? plan.tiles : 1024);
+      blocks = plan.tiles < 1024 ? plan.tiles : 1024;
       break;
     // One run: copy_exact's geometry (a 16-byte vector per thread). Rows as
     // 16-byte units, one per thread, when the row plan applies.
@@ -325,9 +322,7 @@ int move_route(const View& src, const long long* dst_strides, long long dst_offs
                  : T4A_MOVE_ROUTE_ELEMENTS;
     case t4a::kMoveTiled:
       if (t4a::transpose_route(plan, &tr)) return T4A_MOVE_ROUTE_TRANSPOSE;
-      if (es >= 4 && static_cast<long long>(launch.grid[0]) == plan.tiles &&
-          t4a::tile_plan(&tp, plan, es))
-        return T4A_MOVE_ROUTE_TILE_ONCE;
+      if (es >= 4 && t4a::tile_plan(&tp, plan, es)) return T4A_MOVE_ROUTE_TILE_ONCE;
       return T4A_MOVE_ROUTE_TILES;
     default: return T4A_MOVE_ROUTE_ELEMENTS;
   }
