@@ -74,33 +74,32 @@ HBM_PEAK_GBPS = 8000.0
 ROTATE = 3
 METRIC = "effective GB/s + % HBM roofline: transpose, strided permute, axis reduce"
 
-# HBM bytes per launch of an operation's dominant kernel, from two rocprofv3
-# --pmc passes over `bench.py --workload W --kernel-only OP` (FETCH_SIZE, then
-# WRITE_SIZE, KiB per dispatch averaged over the launches), each multiplied by
-# the copy calibration: copy_exact of 256 MiB reads and writes 268435456 bytes,
-# and the factor is that over what the counter reports for it. A kernel change
-# needs a new measurement; until then the entry is left out and traffic is null.
+# HBM bytes per launch of an operation's dominant kernel, from one rocprofv3
+# --pmc pass over `bench.py --workload W --kernel-only OP` counting the TCC's
+# DRAM requests by size (TCC_EA0_RDREQ / _RDREQ_32B and TCC_EA0_WRREQ /
+# _WRREQ_64B, summed over the 16 channels x 8 XCDs, averaged over the
+# launches): reads are 128 bytes unless counted as 32-byte requests, writes 64
+# bytes when counted as such and 32 otherwise -- no calibration factor: by this
+# count copy_exact of 256 MiB (268,435,456 bytes a side) reads 268,465,792 and
+# writes 268,673,003. A kernel change needs a new measurement; until then the
+# entry is left out and traffic is null.
+SRC = "profiles/traffic_default_workload_requests.md"
 TRAFFIC: dict[str, dict] = {
-    "sum_i64_inner": {"bytes": 538948628, "source": "profiles/traffic_c2_sum_i64_inner.md"},
-    "sum_f32_inner": {"bytes": 269794476, "source": "profiles/traffic_c2_sum_f32_inner.md"},
-    "sum_f32_outer": {"bytes": 269562792, "source": "profiles/traffic_c2_sum_f32_outer.md"},
-    "transpose_f32_8192": {"bytes": 536952925,
-                           "source": "profiles/traffic_c1big_transpose_f32_8192.md"},
-    "permute4_F64": {"bytes": 268455680, "source": "profiles/traffic_c3_permute4_F64.md"},
-    "sumsq_f32_middle": {"bytes": 539009101, "source": "profiles/traffic_c4_sumsq_f32_middle.md"},
-    "prod_i32_last": {"bytes": 671012891, "source": "profiles/traffic_c4_prod_i32_last.md"},
-    "permute6_c64": {"bytes": 537005613, "source": "profiles/traffic_c5_permute6_c64.md"},
-    "contiguous_to_view_f32_transposed": {
-        "bytes": 536883971, "source": "profiles/traffic_entries_contiguous_to_view_f32_transposed.md"},
-    "broadcast_in_dim_f32_rows": {
-        "bytes": 268405994, "source": "profiles/traffic_entries_broadcast_in_dim_f32_rows.md"},
-    "concatenate_copy_f32_inner": {
-        "bytes": 268421058, "source": "profiles/traffic_entries_concatenate_copy_f32_inner.md"},
-    "concatenate_copy_f32_outer": {
-        "bytes": 268472325, "source": "profiles/traffic_entries_concatenate_copy_f32_outer.md"},
-    "fill_zero_f32": {"bytes": 268378148, "source": "profiles/traffic_entries_fill_zero_f32.md"},
-    "fill_zero_view_f32_rows": {
-        "bytes": 268247785, "source": "profiles/traffic_entries_fill_zero_view_f32_rows.md"},
+    "transpose_f32_1024": {"bytes": 8473600, "source": SRC},
+    "transpose_f32_8192": {"bytes": 537184661, "source": SRC},
+    "sum_f32_inner": {"bytes": 269825557, "source": SRC},
+    "max_f32_inner": {"bytes": 269906309, "source": SRC},
+    "sum_f32_outer": {"bytes": 269590293, "source": SRC},
+    "max_f32_outer": {"bytes": 269615637, "source": SRC},
+    "sum_i64_inner": {"bytes": 539006283, "source": SRC},
+    "permute4_F64": {"bytes": 268540693, "source": SRC},
+    "permute4_C32": {"bytes": 268574571, "source": SRC},
+    "sumsq_f32_middle": {"bytes": 539053083, "source": SRC},
+    "min_f32_middle": {"bytes": 539098752, "source": SRC},
+    "prod_i32_last": {"bytes": 671134592, "source": SRC},
+    "permute6_c64": {"bytes": 537073323, "source": SRC},
+    "sum_c64_axis3": {"bytes": 285289195, "source": SRC},
+    "copy_f32_256MiB": {"bytes": 537138795, "source": SRC},
 }
 
 NUMPY_DTYPE = {t.DType.F32: np.float32, t.DType.F64: np.float64, t.DType.I32: np.int32,
@@ -894,6 +893,9 @@ def main() -> None:
             "kernel": op.kernel, "kernel_ms": round(k_ms, 5),
             "kernel_GBps": round(op.dominant_bytes / (k_ms * 1e-3) / 1e9, 1),
             "kernel_frac": round(frac, 4)}
+        if op.name in TRAFFIC:
+            cfg["ops"][op.name]["kernel_traffic_ratio"] = round(
+                TRAFFIC[op.name]["bytes"] / op.dominant_bytes, 4)
         if dom is None or k_ms > dom[1]:
             dom = (op, k_ms)
     for cfg in breakdown.values():
