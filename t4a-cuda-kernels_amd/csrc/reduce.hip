@@ -1736,12 +1736,15 @@ struct AnySideScratch {
   int axis8;
 };
 
-__device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, AnySideScratch* tmp,
-                                             int dtype, const void* in,
+// On a contiguous axis the same plan may instead be the lean mapping's: then
+// the LeanPlan goes to `lean` and the result is minus its slot count.
+__device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, t4a::LeanPlan* lean,
+                                             AnySideScratch* tmp, int dtype, int op,
+                                             const void* in,
                                              const t4a_cuda_layout_any& partials,
                                              const t4a_cuda_layout_any& input, int axis,
                                              long long output_len, long long splits,
-                                             long long chunk_len) {
+                                             long long chunk_len, bool whole_waves) {
   if (!t4a::sideways_dtype(dtype) || axis < 0 || axis >= input.rank ||
       partials.rank != input.rank)
     return 0;
@@ -1752,11 +1755,20 @@ __device__ __forceinline__ int any_side_plan(t4a::SidePlan* side, AnySideScratch
   const int axis8 = tmp->axis8;
   const uintptr_t address = reinterpret_cast<uintptr_t>(in);
   const int align = (address & 15) == 0 ? 16 : (address & 7) == 0 ? 8 : (address & 3) == 0 ? 4 : 1;
-  t4a::partials_plan(&tmp->pp, tmp->p8, tmp->i8, axis8, output_len, splits, t4a::kWarp, 1,
-                     t4a::dtype_size(dtype), align);
-  if (tmp->pp.mode != t4a::kPartialsTiles) return 0;
-  t4a::side_plan_into(side, tmp->pp, splits, chunk_len);
-  return tmp->pp.cpl;
+  t4a::partials_plan(&tmp->pp, tmp->p8, tmp->i8, axis8, output_len, splits, t4a::kWarp,
+                     whole_waves ? 1 : 0, t4a::dtype_size(dtype), align);
+  if (tmp->pp.mode == t4a::kPartialsTiles) {
+    t4a::side_plan_into(side, tmp->pp, splits, chunk_len);
+    return tmp->pp.cpl;
+  }
+  if (tmp->pp.mode == t4a::kPartialsPlane && align == 16) {
+    const int k = t4a::lean_slots(tmp->pp, dtype, op, splits, chunk_len, t4a::kWarp);
+    if (k > 0) {
+      *lean = t4a::lean_plan(tmp->pp, splits, chunk_len);
+      return -k;
+    }
+  }
+  return 0;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
@@ -1766,7 +1778,10 @@ extern "C" __global__ void __launch_bounds__(256)
                                  long long splits, long long chunk_len) {
   __shared__ t4a::ReduceDimsWide rd;
   __shared__ t4a::SidePlan side;
+  __shared__ t4a::LeanPlan lean;
   __shared__ AnySideScratch side_tmp;
+  // > 0: TILES with that many columns per lane; < 0: LEAN with minus that
+  // many slots; 0: planes
   __shared__ int side_cpl;
   __shared__ alignas(16) unsigned char tiles_lds[(t4a::kBlock / t4a::kWave) * t4a::kWave * 2 * 8];
   __shared__ int redo;
@@ -1774,16 +1789,43 @@ extern "C" __global__ void __launch_bounds__(256)
   const unsigned int blocks = t4a::entry_blocks(t4a::partials_entry_waves());
   const bool whole_waves = blockDim.x == static_cast<unsigned>(t4a::kBlock) &&
                            blockDim.y == 1 && blockDim.z == 1;
+  // The lean walk's planes: 32-lane planes filling 1-D blocks, a stride of
+  // at most 2^24 planes (its 32-bit cube indices).
+  const bool plane_blocks = blockDim.x % 32u == 0 && blockDim.y == 1 && blockDim.z == 1 &&
+                            static_cast<unsigned long long>(blocks) * (blockDim.x / 32u) <=
+                                (1ull << 24);
   if (threadIdx.x == 0) {
     any_dims(&rd, partials_layout, in_layout, axis);
-    // Only a strided axis can take the column mapping.
-    side_cpl = rd.n >= 0 && whole_waves && rd.axis_stride != 1
-                   ? any_side_plan(&side, &side_tmp, dtype, in, partials_layout, in_layout,
-                                   axis, output_len, splits, chunk_len)
+    // A strided axis can take the column mapping (whole wavefronts), a
+    // contiguous one the lean mapping.
+    const bool strided = rd.axis_stride != 1;
+    side_cpl = rd.n >= 0 && (strided ? whole_waves : plane_blocks)
+                   ? any_side_plan(&side, &lean, &side_tmp, dtype, op, in, partials_layout,
+                                   in_layout, axis, output_len, splits, chunk_len,
+                                   strided && whole_waves)
                    : 0;
   }
   __syncthreads();
   if (rd.n < 0) return;
+  if (side_cpl < 0) {
+    const t4a::LeanPlan& lp = lean;  // from LDS
+    const int k = -side_cpl;
+    t4a::dispatch_dtype(dtype, [&](auto* tag) {
+      using T = std::remove_pointer_t<decltype(tag)>;
+      if constexpr (t4a::VecLanes<T>::value > 0) {
+        t4a::dispatch_fold<T>(op, [&](auto fold) {
+          using F = decltype(fold);
+          switch (k) {
+            case 1: t4a::partials_lean_entry<F, T, 1, 4>(partials, in, lp, fold, blocks); break;
+            case 2: t4a::partials_lean_entry<F, T, 2, 4>(partials, in, lp, fold, blocks); break;
+            case 3: t4a::partials_lean_entry<F, T, 3, 2>(partials, in, lp, fold, blocks); break;
+            default: t4a::partials_lean_entry<F, T, 4, 2>(partials, in, lp, fold, blocks); break;
+          }
+        });
+      }
+    });
+    return;
+  }
   if (side_cpl > 0) {
     const t4a::SidePlan& sp = side;  // from LDS (copied to scalar registers it spills)
     const int cpl = side_cpl;

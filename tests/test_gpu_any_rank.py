@@ -407,3 +407,55 @@ def test_strided_axis_pass1_twin_takes_the_column_mapping(dtype):
                 ga, gb = to_host(a, pn * dtype.size), to_host(b, pn * dtype.size)
                 assert np.array_equal(gb, ga), (ext, shift, rank, op)
                 assert np.array_equal(ga, want.view(np.uint8)), (ext, shift, rank, op)
+
+
+@pytest.mark.parametrize("dtype", [F32, F64, DType.I32, DType.I64], ids=lambda d: d.name)
+def test_contiguous_axis_pass1_twin_takes_the_lean_mapping(dtype):
+    """A pass 1 over a contiguous axis in short chunks: the twin plans the lean
+    mapping inside the kernel (several chunks' loads in flight per plane). At
+    rank 9 and rank 2 through the twin, its partials are the by-value
+    launcher's and the oracle's bytes, for every op the dtype has, equal and
+    ragged last chunks, aligned and shifted (no lean) inputs, one and several
+    fused output dims."""
+    rng = np.random.default_rng(91)
+    ops = [ReduceOp.Sum, ReduceOp.Max, ReduceOp.Min, ReduceOp.Prod]
+    if dtype in (F32, F64):
+        ops.append(ReduceOp.SumSquares)
+    for ext, shift in (([8192, 96], 0), ([5000, 64], 0), ([8192, 24, 5], 0), ([4096, 80], 1)):
+        axis = 0
+        n = count(ext)
+        if dtype in (DType.I32, DType.I64):
+            src = rng.integers(-3, 4, n + shift).astype(NUMPY[dtype])
+        else:
+            src = rng.uniform(-1, 1, n + shift).astype(NUMPY[dtype])
+        d_src = to_device(src)
+        fi = Layout(list(ext), Layout.compact(ext).strides, shift)
+        out_ext = [1] + list(ext[1:])
+        on = count(out_ext)
+        split = t.split_policy(ext[0], 32)
+        pl = t.reduction_partials_layout(Layout.compact(ext), axis, split.splits)
+        pn = pl.element_count()
+        r0 = len(ext)
+        for rank in (r0, 9):
+            k = rank - r0
+            wi = WideLayout(list(ext) + [1] * k, fi.strides + [5] * k, shift)
+            wp = WideLayout(pl.extents + [1] * k, pl.strides + [5] * k, 0)
+            gi, gp = Geometry(wi), Geometry(wp)
+            for op in ops:
+                plan = t.plan_reduce_partials(dtype, op, pl, pn, fi, n + shift, axis, split, 32)
+                aplan = t.plan_reduce_partials(dtype, op, wp, pn, wi, n + shift, axis, split, 32)
+                if rank == 9:
+                    assert aplan.variant == t.RankVariant.General
+                say("contiguous pass-1 twin", dtype.name, ext, shift, rank, op.name,
+                    split.splits, split.chunk_len, aplan.grid)
+                a, b = sentinel(pn * dtype.size), sentinel(pn * dtype.size)
+                hip.reduce_partials(a, d_src, dtype, op, pl, fi, axis, on, split.splits,
+                                    split.chunk_len, plan, stream())
+                hip.reduce_partials_any(b, d_src, dtype, op, gp.c, gi.c, axis, on, split.splits,
+                                        split.chunk_len, aplan, stream())
+                want = np.zeros(pn, dtype=NUMPY[dtype])
+                orc.reduce_partials(want, src, dtype, op, 32, pl, fi, axis, on, split.splits,
+                                    split.chunk_len)
+                ga, gb = to_host(a, pn * dtype.size), to_host(b, pn * dtype.size)
+                assert np.array_equal(gb, ga), (ext, shift, rank, op)
+                assert np.array_equal(ga, want.view(np.uint8)), (ext, shift, rank, op)
