@@ -838,8 +838,14 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
                   "the tile and its plan share the move scratch");
     if (blockDim.x == static_cast<unsigned>(kBlock)) {
       TilePlan* shared_tp = reinterpret_cast<TilePlan*>(lds + kTileBytes);
+      // 0: no TilePlan form; 1: wide slot offsets; 2: narrow ones.
       __shared__ int once_ok;
-      if (threadIdx.x == 0) once_ok = tile_plan(shared_tp, p, static_cast<int>(sizeof(P))) ? 1 : 0;
+      if (threadIdx.x == 0) {
+        once_ok = tile_plan(shared_tp, p, static_cast<int>(sizeof(P)))
+                      ? (tile_offsets_narrow(*shared_tp, LA, LB, static_cast<int>(sizeof(P))) ? 2
+                                                                                          : 1)
+                      : 0;
+      }
       __syncthreads();
       if (once_ok) {
         constexpr int V = tile_vector<P>();
@@ -851,9 +857,26 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
         // scalar file, and the spills into vector registers halve the
         // occupancy of every path of the entry kernel.
         const TilePlan& tp = *shared_tp;
+        // Every block of a grid the chip holds at once works (this build's
+        // planned grids): the fully vectorized shapes then take the
+        // launchers' pipelined walk. Under the reference's per-element grids,
+        // where returning blocks need the free slots, one tile at a time
+        // measured faster.
+        const bool resident = blocks == gridDim.x &&
+                              static_cast<unsigned long long>(gridDim.x) *
+                                      ((blockDim.x + 63u) / 64u) <=
+                                  kEntryResidentWaves;
+        const bool narrow = once_ok == 2;
         auto walk = [&](auto vl_tag, auto vs_tag) {
           constexpr int VLt = decltype(vl_tag)::value;
           constexpr int VSt = decltype(vs_tag)::value;
+          if constexpr (VLt == V && VSt == V) {
+            if (resident && narrow) {
+              move_tile_walk<P, VLt, VSt, LA, LB, TilePlan, true, true>(
+                  static_cast<P*>(dst), static_cast<const P*>(src), tp, tile, tiles, blocks);
+              return;
+            }
+          }
           move_tile_walk<P, VLt, VSt, LA, LB, TilePlan, false, false>(
               static_cast<P*>(dst), static_cast<const P*>(src), tp, tile, tiles, blocks);
         };

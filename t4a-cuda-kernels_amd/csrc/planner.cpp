@@ -651,12 +651,27 @@ int plan_concatenate(int dtype, const View& out, long long out_len, const View& 
 // per CU): 4.1-5.0 TB/s, against 3.0-4.2 at 256, 3.6-4.7 at 1024 and 2.7-4.2
 // at 2048.
 constexpr unsigned kAnyMoveBlocks = 512;
+// Moves on the row route (a dim contiguous on both sides, or one run) keep
+// 1024: the rank-9 8192^2 f32 row copy took 97 us there against 114 at 512,
+// while the tiled ones were slower at 1024 (C3 64 against 60 us, the 8192^2
+// transpose 112 against 105).
+constexpr unsigned kAnyRowBlocks = 1024;
 
-int general_movement(int status, t4a_launch* launch) {
-  if (status == T4A_OK && launch->variant == T4A_VARIANT_GENERAL &&
-      launch->grid[0] > kAnyMoveBlocks)
-    launch->grid[0] = kAnyMoveBlocks;
+int general_movement(int status, t4a_launch* launch, unsigned cap = kAnyMoveBlocks) {
+  if (status == T4A_OK && launch->variant == T4A_VARIANT_GENERAL && launch->grid[0] > cap)
+    launch->grid[0] = cap;
   return status;
+}
+
+// The block cap of a GENERAL move of `src` into dst_strides / dst_offset
+// (nullptr: the compact destination), by the route its fused plan takes.
+unsigned any_move_cap(int dtype, const View& src, const long long* dst_strides,
+                      long long dst_offset) {
+  long long len;
+  if (element_count(src, &len) != T4A_OK) return kAnyMoveBlocks;
+  const int r = move_route(src, dst_strides, dst_offset, len, t4a::dtype_size(dtype));
+  return r == T4A_MOVE_ROUTE_ROWS || r == T4A_MOVE_ROUTE_LINEAR ? kAnyRowBlocks
+                                                                : kAnyMoveBlocks;
 }
 
 // The same for the reduction twins (thread 0 fuses the geometry per block;
@@ -768,7 +783,10 @@ int t4a_plan_materialize_strided_any(int dtype, const t4a_cuda_layout_any* src,
                                      long long src_len, t4a_launch* launch) {
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_any(src)) return s;
-  return general_movement(plan_materialize(dtype, V(src), src_len, launch), launch);
+  const int status = plan_materialize(dtype, V(src), src_len, launch);
+  return general_movement(status, launch,
+                          status == T4A_OK ? any_move_cap(dtype, V(src), nullptr, 0)
+                                           : kAnyMoveBlocks);
 }
 
 // Reference plan_strided_to_strided (src/lib.rs:1660-1679).
@@ -814,7 +832,11 @@ int t4a_plan_strided_to_strided_any(int dtype, const t4a_cuda_layout_any* src,
   if (launch == nullptr) return T4A_HIP_ERR_NULL_ARGUMENT;
   if (int s = check_any(src)) return s;
   if (int s = check_any(dst)) return s;
-  return general_movement(plan_strided(dtype, V(src), src_len, V(dst), dst_len, launch), launch);
+  const int status = plan_strided(dtype, V(src), src_len, V(dst), dst_len, launch);
+  return general_movement(status, launch,
+                          status == T4A_OK ? any_move_cap(dtype, V(src), V(dst).strides,
+                                                          V(dst).offset)
+                                           : kAnyMoveBlocks);
 }
 
 // Reference TransposeConfig::new (src/lib.rs:471-491).
