@@ -96,7 +96,7 @@ TRAFFIC: dict[str, dict] = {
     "permute4_C32": {"bytes": 268574571, "source": SRC},
     "sumsq_f32_middle": {"bytes": 539053083, "source": SRC},
     "min_f32_middle": {"bytes": 539098752, "source": SRC},
-    "prod_i32_last": {"bytes": 671134592, "source": SRC},
+    "prod_i32_last": {"bytes": 671129643, "source": SRC},
     "permute6_c64": {"bytes": 537073323, "source": SRC},
     "sum_c64_axis3": {"bytes": 285289195, "source": SRC},
     "copy_f32_256MiB": {"bytes": 537138795, "source": SRC},
