@@ -257,6 +257,43 @@ def test_unit_one_group_axes_many_outputs(dtype):
                          explicit=(t.ReduceStrategy.Unit, 32))
 
 
+@pytest.mark.parametrize("dtype", [F32, F64, I32, I64], ids=lambda d: d.name)
+def test_unit_one_group_output_decodes(dtype):
+    """The one-group kernel's two output decodes: one fused output dim with a
+    non-unit output stride (the linear decode), two and three unfused output
+    dims over a padded input (the general decode), each with more than 262,144
+    outputs so the planner's 256-thread Unit launch takes that kernel; and one
+    output under a caller's 256-thread launch (the linear decode with no dim)."""
+    rng = np.random.default_rng(40 + int(dtype))
+    v = 16 // dtype.size
+    length, lp = v + 1, 2 * v  # one group plus one element; rows padded to 2 groups
+    s2 = 67 * lp + v
+    cases = [
+        (t.Layout.compact([length, 300_001]), t.Layout([1, 300_001], [1, 3], 0)),
+        (t.Layout([length, 1001, 300], [1, lp, 1001 * lp + v], 0),
+         t.Layout.compact([1, 1001, 300])),
+        (t.Layout([length, 67, 71, 73], [1, lp, s2, s2 * 71 + v], 0),
+         t.Layout.compact([1, 67, 71, 73])),
+    ]
+    for op in (Sum, Prod, Max):
+        for in_l, out_l in cases:
+            span = in_l.max_reachable_offset() + 1
+            data = values(dtype, op, span, rng)
+            run(dtype, op, in_l, 0, out_l, 32, data, explicit=(t.ReduceStrategy.Unit, 32))
+        # one output, the caller's own 256-thread launch
+        in_l, out_l = t.Layout.compact([length]), t.Layout.compact([1])
+        data = values(dtype, op, length, rng)
+        say("reduce one output", dtype.name, op.name, "length", length)
+        d_in = to_device(data)
+        d_out = sentinel(dtype.size)
+        launch = t.Launch((1, 1, 1), (256, 1, 1), 0)
+        hip.reduce(d_out, d_in, dtype, op, t.ReduceStrategy.Unit, out_l, in_l, 0, 1, launch,
+                   stream())
+        want = np.zeros(1, dtype=NUMPY[dtype])
+        orc.reduce(want, data, dtype, op, t.ReduceStrategy.Unit, 32, out_l, in_l, 0, 1)
+        assert _nan_equal(dtype, to_host(d_out, dtype.size, "output"), want.view(np.uint8))
+
+
 def test_extrema_nan_payloads_bit_exact():
     """Max / Min select an operand, so their results are exact bytes even for NaN
     payloads: several payloads (quiet, signalling, negative) in one chunk, in
