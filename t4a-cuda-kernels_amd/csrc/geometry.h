@@ -680,14 +680,32 @@ T4A_HD TilePlanCompact compact_tile_plan(const TilePlan& tp) {
   return c;
 }
 
-// Compile-time tile shapes, the planner's full tiles when both chains reach
-// their targets: 64 x 64 for 4-byte elements, 64 x 32 for 8-byte ones and
-// 32 x 32 for 16-byte ones.
-T4A_HD bool tile_once_shape(long long la, long long lb, int esize) {
+// Compile-time tile shapes (LA x LB: A the destination run, B the source
+// run). The balanced shape of each element size is the planner's full tile
+// when both chains reach their targets: 64 x 64 for 4-byte elements, 64 x 32
+// for 8-byte ones and 32 x 32 for 16-byte ones; every walk (the launchers'
+// and the entries') has it. When one chain ends at 16 or 32 elements the
+// planner hands the tile budget to the other run, and the launchers also walk
+// those long-and-short shapes, with compact narrow plans (a TILED move with a
+// 32-element source run, as a reversed-view f32 permute has, otherwise takes
+// the general tiled kernel at two thirds of the speed).
+T4A_HD bool tile_balanced_shape(long long la, long long lb, int esize) {
   if (esize == 4) return la == 64 && lb == 64;
   if (esize == 8) return la == 64 && lb == 32;
   if (esize == 16) return la == 32 && lb == 32;
   return false;
+}
+
+T4A_HD bool tile_long_short_shape(long long la, long long lb, int esize) {
+  if (esize == 4)
+    return (la == 128 && (lb == 32 || lb == 16)) || (lb == 128 && (la == 32 || la == 16));
+  if (esize == 8) return (la == 128 && lb == 16) || (la == 16 && lb == 128) || (la == 32 && lb == 64);
+  if (esize == 16) return (la == 64 && lb == 16) || (la == 16 && lb == 64);
+  return false;
+}
+
+T4A_HD bool tile_once_shape(long long la, long long lb, int esize) {
+  return tile_balanced_shape(la, lb, esize) || tile_long_short_shape(la, lb, esize);
 }
 
 T4A_HD bool tile_plan(TilePlan* tp, const MovePlan& p, int esize) {
@@ -732,6 +750,15 @@ T4A_HD bool tile_plan(TilePlan* tp, const MovePlan& p, int esize) {
   }
   for (int q = 0; q < tp->ncoord; ++q) tp->coord[q] = p.coord_div[q];
   return true;
+}
+
+// Whether the launchers walk a tile plan with one of the walk kernels: the
+// balanced shape in any plan form, a long-and-short one in the compact narrow
+// form only (anything else takes the general tiled kernel).
+T4A_HD bool tile_walk_applies(const MovePlan& p, const TilePlan& tp, int esize) {
+  if (tile_balanced_shape(p.la, p.lb, esize)) return true;
+  return tile_long_short_shape(p.la, p.lb, esize) && tp.ncoord <= kCompactCoords &&
+         tile_offsets_narrow(tp, static_cast<int>(p.la), static_cast<int>(p.lb), esize);
 }
 
 // ---- reductions ---------------------------------------------------------------

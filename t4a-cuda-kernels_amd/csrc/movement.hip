@@ -840,8 +840,9 @@ __device__ __forceinline__ void move_tiled_entry(void* dst, const void* src, con
       TilePlan* shared_tp = reinterpret_cast<TilePlan*>(lds + kTileBytes);
       // 0: no TilePlan form; 1: wide slot offsets; 2: narrow ones.
       __shared__ int once_ok;
+      // The entries walk the balanced shape only.
       if (threadIdx.x == 0) {
-        once_ok = tile_plan(shared_tp, p, static_cast<int>(sizeof(P)))
+        once_ok = p.la == LA && p.lb == LB && tile_plan(shared_tp, p, static_cast<int>(sizeof(P)))
                       ? (tile_offsets_narrow(*shared_tp, LA, LB, static_cast<int>(sizeof(P))) ? 2
                                                                                           : 1)
                       : 0;
@@ -1561,30 +1562,57 @@ void launch_tile_walk(unsigned int tiles, hipStream_t s, void* dst, const void* 
                      dst, src, tp, tiles);
 }
 
-template <typename P, int VL, int VS>
-void launch_tile_shape(unsigned int tiles, hipStream_t s, void* dst, const void* src,
-                       const t4a::TilePlan& tp) {
-  constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
-  constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
-  if (tp.ncoord <= t4a::kCompactCoords &&
-      t4a::tile_offsets_narrow(tp, LA, LB, static_cast<int>(sizeof(P))))
-    launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>>(
-        tiles, s, dst, src, t4a::compact_tile_plan(tp));
-  else
-    launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlan, false>>(
-        tiles, s, dst, src, tp);
+// A long-and-short LA x LB tile: compact narrow plans only
+// (t4a::tile_walk_applies has checked the form).
+template <typename P, int VL, int VS, int LA, int LB>
+void launch_walk_compact(unsigned int tiles, hipStream_t s, void* dst, const void* src,
+                         const t4a::TilePlan& tp) {
+  launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>>(
+      tiles, s, dst, src, t4a::compact_tile_plan(tp));
 }
 
-// The one-tile kernels by vector widths (t4a::tile_once_shape's shapes).
-template <typename P, int V>
-void launch_tile_once(bool vl, bool vs, unsigned int tiles, hipStream_t s, void* dst,
-                      const void* src, const t4a::TilePlan& tp) {
-  if constexpr (V > 1) {
-    if (vl && vs) return launch_tile_shape<P, V, V>(tiles, s, dst, src, tp);
-    if (vl) return launch_tile_shape<P, V, 1>(tiles, s, dst, src, tp);
-    if (vs) return launch_tile_shape<P, 1, V>(tiles, s, dst, src, tp);
+// The walk kernel of the plan's tile shape (la x lb, one of
+// t4a::tile_once_shape's) and vector widths.
+template <typename P, int VL, int VS>
+void launch_tile_shape(long long la, long long lb, unsigned int tiles, hipStream_t s, void* dst,
+                       const void* src, const t4a::TilePlan& tp) {
+  constexpr int LA = sizeof(P) >= 16 ? 32 : 64;
+  constexpr int LB = sizeof(P) >= 8 ? 32 : 64;
+  if (la == LA && lb == LB) {
+    if (tp.ncoord <= t4a::kCompactCoords &&
+        t4a::tile_offsets_narrow(tp, LA, LB, static_cast<int>(sizeof(P))))
+      launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>>(
+          tiles, s, dst, src, t4a::compact_tile_plan(tp));
+    else
+      launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlan, false>>(
+          tiles, s, dst, src, tp);
+    return;
   }
-  launch_tile_shape<P, 1, 1>(tiles, s, dst, src, tp);
+  if constexpr (sizeof(P) == 4) {
+    if (la == 128 && lb == 32) return launch_walk_compact<P, VL, VS, 128, 32>(tiles, s, dst, src, tp);
+    if (la == 128 && lb == 16) return launch_walk_compact<P, VL, VS, 128, 16>(tiles, s, dst, src, tp);
+    if (la == 32 && lb == 128) return launch_walk_compact<P, VL, VS, 32, 128>(tiles, s, dst, src, tp);
+    if (la == 16 && lb == 128) return launch_walk_compact<P, VL, VS, 16, 128>(tiles, s, dst, src, tp);
+  } else if constexpr (sizeof(P) == 8) {
+    if (la == 128 && lb == 16) return launch_walk_compact<P, VL, VS, 128, 16>(tiles, s, dst, src, tp);
+    if (la == 16 && lb == 128) return launch_walk_compact<P, VL, VS, 16, 128>(tiles, s, dst, src, tp);
+    if (la == 32 && lb == 64) return launch_walk_compact<P, VL, VS, 32, 64>(tiles, s, dst, src, tp);
+  } else if constexpr (sizeof(P) == 16) {
+    if (la == 64 && lb == 16) return launch_walk_compact<P, VL, VS, 64, 16>(tiles, s, dst, src, tp);
+    if (la == 16 && lb == 64) return launch_walk_compact<P, VL, VS, 16, 64>(tiles, s, dst, src, tp);
+  }
+}
+
+// The walk kernels by vector widths.
+template <typename P, int V>
+void launch_tile_once(bool vl, bool vs, long long la, long long lb, unsigned int tiles,
+                      hipStream_t s, void* dst, const void* src, const t4a::TilePlan& tp) {
+  if constexpr (V > 1) {
+    if (vl && vs) return launch_tile_shape<P, V, V>(la, lb, tiles, s, dst, src, tp);
+    if (vl) return launch_tile_shape<P, V, 1>(la, lb, tiles, s, dst, src, tp);
+    if (vs) return launch_tile_shape<P, 1, V>(la, lb, tiles, s, dst, src, tp);
+  }
+  launch_tile_shape<P, 1, 1>(la, lb, tiles, s, dst, src, tp);
 }
 
 // A compact 2-D transpose found in a movement plan, on the tiled transpose's
@@ -1683,8 +1711,10 @@ int launch_move(void* dst, const void* src, const t4a::MovePlan& plan,
     if constexpr (sizeof(P) >= 4) {
       t4a::TilePlan tp;
       if (block.x == static_cast<unsigned>(t4a::kBlock) && block.y == 1 && block.z == 1 &&
-          grid.y == 1 && grid.z == 1 && t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P)))) {
-        launch_tile_once<P, V>(vl, vs, static_cast<unsigned int>(plan.tiles), s, dst, src, tp);
+          grid.y == 1 && grid.z == 1 && t4a::tile_plan(&tp, plan, static_cast<int>(sizeof(P))) &&
+          t4a::tile_walk_applies(plan, tp, static_cast<int>(sizeof(P)))) {
+        launch_tile_once<P, V>(vl, vs, plan.la, plan.lb, static_cast<unsigned int>(plan.tiles), s,
+                               dst, src, tp);
         return status_of_last_launch();
       }
     }

@@ -322,7 +322,8 @@ int move_route(const View& src, const long long* dst_strides, long long dst_offs
                  : T4A_MOVE_ROUTE_ELEMENTS;
     case t4a::kMoveTiled:
       if (t4a::transpose_route(plan, &tr)) return T4A_MOVE_ROUTE_TRANSPOSE;
-      if (es >= 4 && t4a::tile_plan(&tp, plan, es)) return T4A_MOVE_ROUTE_TILE_ONCE;
+      if (es >= 4 && t4a::tile_plan(&tp, plan, es) && t4a::tile_walk_applies(plan, tp, es))
+        return T4A_MOVE_ROUTE_TILE_ONCE;
       return T4A_MOVE_ROUTE_TILES;
     default: return T4A_MOVE_ROUTE_ELEMENTS;
   }

@@ -224,6 +224,36 @@ def test_strided_to_strided_random_views(dtype):
         run_strided(dtype, src, t.Layout(ext, st, int(rng.integers(0, 7))), rng)
 
 
+def _strides(ext, order):
+    st, c = [0] * len(ext), 1
+    for k in order:
+        st[k] = c
+        c *= ext[k]
+    return st
+
+
+@pytest.mark.parametrize("dtype", [t.DType.F32, t.DType.I32, t.DType.F64, t.DType.C32,
+                                   t.DType.C64], ids=lambda d: d.name)
+def test_long_and_short_tiles(dtype):
+    """Moves whose run ends at 16 or 32 elements on one side, walked with the
+    long-and-short tiles (128 x 16 ... 16 x 128), full and ragged, with aligned
+    buffers (16-byte vectors on both sides) and with the source or the
+    destination one element off (one side element by element)."""
+    rng = np.random.default_rng(90 + int(dtype))
+    cases = [([64, 32, 16, 8], [2, 0, 3, 1], [0, 1, 2, 3]),
+             ([64, 32, 32, 8], [2, 0, 3, 1], [0, 1, 2, 3]),
+             ([32, 64, 32, 8], [1, 2, 0, 3], [0, 1, 3, 2]),
+             ([16, 64, 32, 8], [1, 2, 0, 3], [0, 1, 3, 2]),
+             ([64, 33, 16, 5], [2, 0, 3, 1], [0, 1, 2, 3]),
+             ([16, 64, 33, 7], [1, 2, 0, 3], [0, 1, 3, 2])]
+    for ext, so, do in cases:
+        for s_off, d_off in ((0, 0), (1, 0), (0, 1)):
+            src = t.Layout(ext, _strides(ext, so), s_off)
+            dst = t.Layout(ext, _strides(ext, do), d_off)
+            assert t.move_route(dtype, src, dst) == t.MoveRoute.TileOnce
+            run_strided(dtype, src, dst, rng)
+
+
 def test_config_c1_transpose_and_its_8192_twin():
     """C1: f32 C-[1024, 1024] transposed (1,0), and the 8192^2 roofline twin, on
     the configuration's seeded inputs (t4a_cuda_kernels.configs)."""

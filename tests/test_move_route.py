@@ -85,6 +85,36 @@ def test_tile_and_element_routes():
     assert route(F32, Layout([], [], 3)) == MoveRoute.Elements
 
 
+def _strides(ext, order):
+    """Strides of a compact buffer whose axes, fastest first, are `order`."""
+    st, c = [0] * len(ext), 1
+    for k in order:
+        st[k] = c
+        c *= ext[k]
+    return st
+
+
+# Moves whose run ends at 16 or 32 elements on one side (the next dim of that
+# side's chain belongs to the other chain), so the planner hands the tile budget
+# to the other run: 128 x 16, 128 x 32, 32 x 128, 16 x 128 tiles for 4-byte
+# elements, 128 x 16, 32 x 64, 16 x 128 for 8-byte, 64 x 16, 16 x 64 for 16-byte.
+LONG_SHORT = [
+    ([64, 32, 16, 8], [2, 0, 3, 1], [0, 1, 2, 3]),
+    ([64, 32, 32, 8], [2, 0, 3, 1], [0, 1, 2, 3]),
+    ([32, 64, 32, 8], [1, 2, 0, 3], [0, 1, 3, 2]),
+    ([16, 64, 32, 8], [1, 2, 0, 3], [0, 1, 3, 2]),
+    ([64, 33, 16, 5], [2, 0, 3, 1], [0, 1, 2, 3]),
+    ([16, 64, 33, 7], [1, 2, 0, 3], [0, 1, 3, 2]),
+]
+
+
+def test_long_and_short_tiles_take_the_tile_walk():
+    for ext, so, do in LONG_SHORT:
+        src, dst = Layout(ext, _strides(ext, so), 0), Layout(ext, _strides(ext, do), 0)
+        for dt in (F32, F64, C32, C64):
+            assert route(dt, src, dst) == MoveRoute.TileOnce, (ext, dt)
+
+
 def test_route_validates_like_the_planners():
     with pytest.raises(T4aError) as e:
         route(F32, Layout.compact([3, 4]), Layout.compact([4, 3]))
