@@ -1563,12 +1563,18 @@ void launch_tile_walk(unsigned int tiles, hipStream_t s, void* dst, const void* 
 }
 
 // A long-and-short LA x LB tile: compact narrow plans only
-// (t4a::tile_walk_applies has checked the form).
+// (t4a::tile_walk_applies has checked the form), one block per tile (the walk
+// then moves one tile a block). On six such moves (2^25 elements of 4, 8 and
+// 16 bytes, a 16-element run on either side) that measured 8-12 % faster than
+// the resident grid; the balanced tiles keep the resident grid,
+// which C5's permute needs (97 us against 107 with a block per tile), although
+// other balanced moves ran 0-13 % faster with a block per tile.
 template <typename P, int VL, int VS, int LA, int LB>
 void launch_walk_compact(unsigned int tiles, hipStream_t s, void* dst, const void* src,
                          const t4a::TilePlan& tp) {
-  launch_tile_walk<t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>>(
-      tiles, s, dst, src, t4a::compact_tile_plan(tp));
+  hipLaunchKernelGGL(
+      (t4a::move_tile_walk_kernel<P, VL, VS, LA, LB, t4a::TilePlanCompact, true>), dim3(tiles),
+      dim3(t4a::kBlock), 0, s, dst, src, t4a::compact_tile_plan(tp), tiles);
 }
 
 // The walk kernel of the plan's tile shape (la x lb, one of
