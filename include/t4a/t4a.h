@@ -144,7 +144,7 @@ typedef enum {
   T4A_MOVE_ROUTE_LINEAR = 1,    /* one run contiguous on both sides: the copy kernel */
   T4A_MOVE_ROUTE_ROWS = 2,      /* a dim contiguous on both sides: 16-byte row units */
   T4A_MOVE_ROUTE_TRANSPOSE = 3, /* one compact 2-D transpose: the tiled transpose's kernel */
-  T4A_MOVE_ROUTE_TILE_ONCE = 4, /* one 16 KiB LDS tile per block */
+  T4A_MOVE_ROUTE_TILE_ONCE = 4, /* LDS tiles of one of the tile walk's shapes */
   T4A_MOVE_ROUTE_TILES = 5,     /* persistent blocks walking LDS tiles */
   T4A_MOVE_ROUTE_ELEMENTS = 6   /* one decode per element */
 } t4a_move_route;

@@ -360,7 +360,7 @@ class MoveRoute(enum.IntEnum):
     Linear = 1     # one run contiguous on both sides: the copy kernel
     Rows = 2       # a dim contiguous on both sides: 16-byte row units
     Transpose = 3  # one compact 2-D transpose: the tiled transpose's kernel
-    TileOnce = 4   # one 16 KiB LDS tile per block
+    TileOnce = 4   # LDS tiles of one of the tile walk's shapes
     Tiles = 5      # persistent blocks walking LDS tiles
     Elements = 6   # one decode per element
 

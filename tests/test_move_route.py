@@ -4,8 +4,8 @@ The planner fuses axes (extent-1 axes dropped, axes chained on both sides
 merged) and then picks the kernel: the copy kernel for one run contiguous on
 both sides (the reference consumer's "linear" class), 16-byte row units when a
 dim is contiguous on both sides, the tiled transpose's kernel for one compact
-2-D transpose, one LDS tile per block when each run's chain has at most two
-dims and the tile is full-size, the persistent tiled walk otherwise, and a
+2-D transpose, the tile walk when each run's chain has at most two dims and
+the tile is one of the walk's shapes, the general tiled kernel otherwise, and a
 per-element decode when no dim is contiguous on one of the sides
 (reference docs/design/cubecl-performance-parity.md:57-63 asks for exactly
 this linear / strided / tiled classification after fusion).
