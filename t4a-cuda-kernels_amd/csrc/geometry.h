@@ -272,6 +272,27 @@ T4A_HD int fuse_move(int rank, const long long* ext, const long long* ss, const 
       [&](int k) { return ds ? ds[k] : cd(k); }, fe, fs, fd, cap);
 }
 
+// GENERIC: one decode per element over the fused dims; in 32-bit arithmetic
+// with multiply-high divisors (coord_div[k] for dim k) when the count and every
+// extent are below 2^31 (a 64-bit division per dim per element otherwise).
+T4A_HD void move_generic(MovePlan* p, long long len) {
+  p->mode = kMoveGeneric;
+  p->tiles = len;
+  bool narrow = len < (1ll << 31);
+  for (int k = 0; k < p->n; ++k) narrow = narrow && p->ext[k] < (1ll << 31);
+  p->coords32 = narrow;
+  if (narrow) {
+    for (int k = 0; k < p->n; ++k)
+      p->coord_div[k] = fast_div(static_cast<unsigned int>(p->ext[k]));
+  }
+}
+
+// Tiles smaller than this many elements (two chains that end at a few
+// elements each, as when a permute swaps small neighbouring axes) move
+// faster one element at a time: an [8]^8 f32 permute swapping axis pairs
+// (8 x 8 tiles) took 881 us through the general tiled kernel.
+constexpr long long kMoveMinTile = 256;
+
 // `dst_strides == nullptr` means the compact destination of materialize_strided.
 // The source is `rank` axes of extents `src_ext` and strides `src_str` (at most
 // kMaxDims are read) from `src_offset`.
@@ -330,8 +351,7 @@ T4A_HD void move_plan_view(MovePlan* p, int rank, long long src_offset, const lo
     return;
   }
   if (a < 0 || b < 0) {
-    p->mode = kMoveGeneric;
-    p->tiles = len;
+    move_generic(p, len);
     return;
   }
   // Tile budget: 16 KiB of elements -- 4096 of 4 bytes or less (runs aiming
@@ -432,6 +452,11 @@ T4A_HD void move_plan_view(MovePlan* p, int rank, long long src_offset, const lo
     p->b_tile = t;
     p->b_tiles = (last + t - 1) / t;
     p->lb = p->b_inner * t;
+  }
+  if (p->la * p->lb < kMoveMinTile) {
+    p->na = p->nb = 0;
+    move_generic(p, len);
+    return;
   }
   long long tiles = p->a_tiles * p->b_tiles;
   for (int k = 0; k < p->n; ++k) {

@@ -792,6 +792,25 @@ __device__ __forceinline__ void move_elements(void* dst, const void* src, const 
   const P* s = static_cast<const P*>(src);
   const int bs = block_threads<BS>();
   const long long gstride = static_cast<long long>(blocks) * bs;
+  if (p.coords32 && gstride < (1ll << 31)) {
+    // f < len < 2^31 and f + gstride < 2^32: 32-bit indices and divisors.
+    const unsigned int len = static_cast<unsigned int>(p.len);
+    for (unsigned int f = blockIdx.x * bs + threadIdx.x; f < len;
+         f += static_cast<unsigned int>(gstride)) {
+      unsigned int rest = f;
+      long long so = p.src_offset;
+      long long dof = p.dst_offset;
+      for (int k = 0; k < p.n; ++k) {
+        const unsigned int q = div_by(rest, p.coord_div[k]);
+        const unsigned int c = rest - q * p.coord_div[k].d;
+        rest = q;
+        so += static_cast<long long>(c) * p.ss[k];
+        dof += static_cast<long long>(c) * p.ds[k];
+      }
+      d[dof] = s[so];
+    }
+    return;
+  }
   for (long long f = static_cast<long long>(blockIdx.x) * bs + threadIdx.x; f < p.len;
        f += gstride) {
     long long rest = f;

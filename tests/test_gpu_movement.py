@@ -254,6 +254,30 @@ def test_long_and_short_tiles(dtype):
             run_strided(dtype, src, dst, rng)
 
 
+def test_general_routes():
+    """The per-element route (tiles below 256 elements, as an [8]^6 permute
+    swapping axis pairs has; a reversed fast axis) and the general tiled kernel
+    (1-byte elements; chains of more than two dims), each on its route, with
+    aligned and shifted buffers."""
+    rng = np.random.default_rng(78)
+    e6, e8 = [8] * 6, [2] * 6 + [64, 64]
+    swap = t.Layout(e6, _strides(e6, [1, 0, 3, 2, 5, 4]), 0)
+    long_chains = t.Layout(e8, _strides(e8, [7, 6, 5, 4, 3, 2, 1, 0]), 0)
+    cases = [(t.DType.F32, swap, t.MoveRoute.Elements),
+             (t.DType.C64, swap, t.MoveRoute.Elements),
+             (t.DType.F32, t.Layout([512, 300], [-1, 512], 511), t.MoveRoute.Elements),
+             (t.DType.Bool, t.Layout([64, 64, 128, 32], [32, 262144, -2048, 1], 260096),
+              t.MoveRoute.Tiles),
+             (t.DType.F32, long_chains, t.MoveRoute.Tiles),
+             (t.DType.F64, long_chains, t.MoveRoute.Tiles)]
+    for dtype, src, want in cases:
+        dst = t.Layout.compact(src.extents)
+        assert t.move_route(dtype, src, dst) == want, (dtype, src)
+        for s_off, d_off in ((0, 0), (1, 3)):
+            run_strided(dtype, t.Layout(src.extents, src.strides, src.offset + s_off),
+                        t.Layout(dst.extents, dst.strides, d_off), rng)
+
+
 def test_config_c1_transpose_and_its_8192_twin():
     """C1: f32 C-[1024, 1024] transposed (1,0), and the 8192^2 roofline twin, on
     the configuration's seeded inputs (t4a_cuda_kernels.configs)."""
