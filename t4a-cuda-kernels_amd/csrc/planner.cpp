@@ -26,6 +26,9 @@ constexpr unsigned kMaxGridX = INT32_MAX;
 constexpr uint64_t kDefaultSharedBytes = 48 * 1024;
 constexpr long long kMinChunkPlanes = 8;
 constexpr long long kMaxSplits = 4096;
+// Blocks of the packed plane launch (256 threads, 8 to 32 planes each): about
+// two rounds of the blocks the device holds at once.
+constexpr long long kPlaneMultiBlocks = 4096;
 constexpr unsigned kMaxBlockWidth = 512;
 constexpr long long kWideCombineMinSplits = 64;
 constexpr long long kCombineTargetFoldsPerLane = 8;
@@ -397,6 +400,28 @@ int plan_reduce(int dtype, int op, int strategy, const View& out, long long out_
   // A one-group axis in kBlock-thread blocks: threads take several outputs.
   t4a_cuda_layout o8, i8;
   int axis8;
+  // PLANE with planes of at most 32 lanes: 256 / W planes a block (block.y),
+  // a grid of at most kPlaneMultiBlocks blocks striding over the outputs, when
+  // the launchers' compact plan takes the outputs (at most three fused dims).
+  if (strategy == T4A_CUDA_REDUCE_PLANE && plane_width <= static_cast<unsigned>(t4a::kWarp) &&
+      output_len > 0 && in.rank <= T4A_CUDA_MAX_RANK &&
+      reduction_pair(out, in, axis, &o8, &i8, &axis8)) {
+    t4a::ReduceDims rd;
+    t4a::reduce_dims(&rd, o8, i8, axis8);
+    const long long planes = kBlock / static_cast<long long>(plane_width);
+    long long blocks = (output_len + planes - 1) / planes;
+    if (blocks > kPlaneMultiBlocks) blocks = kPlaneMultiBlocks;
+    if (t4a::unit_plan_fits(rd, output_len) &&
+        t4a::grid_stride_fits(output_len, static_cast<unsigned int>(blocks),
+                              2ull * static_cast<unsigned long long>(planes))) {
+      launch->grid[0] = static_cast<unsigned int>(blocks);
+      launch->grid[1] = launch->grid[2] = 1;
+      launch->block[0] = plane_width;
+      launch->block[1] = static_cast<unsigned int>(planes);
+      launch->block[2] = 1;
+      launch->shared_bytes = 0;
+    }
+  }
   if (strategy == T4A_CUDA_REDUCE_UNIT && output_len > 0 &&
       launch->block[0] == static_cast<unsigned>(kBlock) &&
       reduction_pair(out, in, axis, &o8, &i8, &axis8)) {

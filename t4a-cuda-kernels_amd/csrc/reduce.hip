@@ -509,6 +509,122 @@ __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, co
   }
 }
 
+// PLANE with planes of W <= 32 lanes packed into 256-thread blocks (threadIdx.x
+// the lane, threadIdx.y the plane; W-aligned lane groups, so the xor tree
+// stays inside each plane): the launchers' geometry for the direct plane
+// reductions of 33..511-element axes, where the reference geometry (one W-lane
+// block per output, which the module entry keeps) leaves half of every
+// wavefront idle and pays one block dispatch per output (2^20 outputs of a
+// 64-element f32 axis: 687 us). Plane p of block b takes outputs
+// b * planes + p + j * S (S = gridDim.x * planes), two at a time with every
+// load of both issued before the first fold when a lane holds at most
+// kAhead / 2 elements of an output; each output is folded exactly as
+// plane_body folds it: lane l seeds element l, folds l + W, l + 2W, ..., then
+// the xor tree.
+template <typename Fold, typename T>
+__device__ __forceinline__ void plane_multi(T* __restrict__ out, const T* __restrict__ in,
+                                            const UnitPlan& up, unsigned int output_len,
+                                            Fold f) {
+  const int w = blockDim.x;
+  const int lane = threadIdx.x;
+  const unsigned int span = gridDim.x * blockDim.y;
+  const int len = up.axis_len;
+  const long long stride = up.axis_stride;
+  constexpr int kAhead = sizeof(T) >= 16 ? 4 : sizeof(T) >= 8 ? 8 : 16;
+  constexpr int kHalf = kAhead / 2;
+  unsigned int o0 = blockIdx.x * blockDim.y + threadIdx.y;
+  if (len <= w * kHalf) {
+    for (; o0 < output_len; o0 += 2 * span) {
+      T v[2][kHalf];
+      long long ob[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const unsigned int o = o0 + u * span;
+        long long ib;
+        unit_decode(up, o < output_len ? o : o0, &ib, &ob[u]);
+        const T* x = in + ib;
+#pragma unroll
+        for (int k = 0; k < kHalf; ++k) {
+          const int i = lane + k * w;
+          if (i < len) v[u][k] = x[i * stride];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        T acc = f.seed(v[u][0]);
+#pragma unroll
+        for (int k = 1; k < kHalf; ++k) {
+          if (lane + k * w < len) acc = f.fold(acc, v[u][k]);
+        }
+        const T reduced = plane_tree(acc, w, f);
+        if (lane == 0 && o0 + u * span < output_len) out[ob[u]] = reduced;
+      }
+    }
+    return;
+  }
+  for (; o0 < output_len; o0 += span) {
+    long long ib, ob;
+    unit_decode(up, o0, &ib, &ob);
+    const T* x = in + ib;
+    T acc;
+    if (len <= w * kAhead) {
+      T v[kAhead];
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) {
+        const int i = lane + k * w;
+        if (i < len) v[k] = x[i * stride];
+      }
+      acc = f.seed(v[0]);
+#pragma unroll
+      for (int k = 1; k < kAhead; ++k) {
+        if (lane + k * w < len) acc = f.fold(acc, v[k]);
+      }
+    } else {
+      acc = f.seed(x[lane * stride]);
+#pragma unroll 4
+      for (long long i = lane + w; i < len; i += w) acc = f.fold(acc, x[i * stride]);
+    }
+    const T reduced = plane_tree(acc, w, f);
+    if (lane == 0) out[ob] = reduced;
+  }
+}
+
+// PLANE of W lanes computed by one thread per output: what lane 0 of that
+// output's plane computes, bit for bit. Lane l folds elements l, l + W, l + 2W,
+// ... (part[l]); the xor tree then leaves in lane 0 the balanced tree of
+// part[0..W) in order (level s combines part[l] with part[l + s], lane 0's own
+// value first: its partner lane l + s holds the same tree of its half). Threads
+// take consecutive outputs, so on a strided axis every load instruction covers
+// neighbouring elements (the planes' loads of one output each touch W lines).
+template <typename Fold, typename T, int W>
+__device__ __forceinline__ void plane_per_thread(T* __restrict__ out, const T* __restrict__ in,
+                                                 const UnitPlan& up, unsigned int output_len,
+                                                 Fold f) {
+  const int len = up.axis_len;
+  const long long stride = up.axis_stride;
+  const unsigned int step = gridDim.x * blockDim.x;
+  for (unsigned int o = blockIdx.x * blockDim.x + threadIdx.x; o < output_len; o += step) {
+    long long ib, ob;
+    unit_decode(up, o, &ib, &ob);
+    const T* x = in + ib;
+    T part[W];
+#pragma unroll
+    for (int l = 0; l < W; ++l) part[l] = f.seed(x[l * stride]);  // len >= W
+    for (int base = W; base < len; base += W) {
+#pragma unroll
+      for (int l = 0; l < W; ++l) {
+        if (base + l < len) part[l] = f.fold(part[l], x[(base + l) * stride]);
+      }
+    }
+#pragma unroll
+    for (int s = 1; s < W; s <<= 1) {
+#pragma unroll
+      for (int l = 0; l < W; l += 2 * s) part[l] = f.combine(part[l], part[l + s]);
+    }
+    out[ob] = part[0];
+  }
+}
+
 // ---- t4a_cuda_reduce_partials -----------------------------------------------------
 
 // Serial lane walk: lane t seeds start + t and folds start + t + kW (reference
@@ -1504,6 +1620,19 @@ __global__ void __launch_bounds__(512)
                       gridDim.x);
 }
 
+template <typename T, typename Fold>
+__global__ void __launch_bounds__(256)
+    reduce_plane_multi_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len) {
+  plane_multi<Fold, T>(static_cast<T*>(out), static_cast<const T*>(in), up, output_len, Fold{});
+}
+
+template <typename T, typename Fold>
+__global__ void __launch_bounds__(256)
+    reduce_plane_thread_kernel(void* out, const void* in, UnitPlan up, unsigned int output_len) {
+  plane_per_thread<Fold, T, kWarp>(static_cast<T*>(out), static_cast<const T*>(in), up,
+                                   output_len, Fold{});
+}
+
 // UNIT with the planner's blocks of BS threads.
 template <typename T, int BS>
 __global__ void __launch_bounds__(BS)
@@ -1956,29 +2085,40 @@ void launch_plane_lean(int op, dim3 grid, dim3 block, hipStream_t s, void* out, 
                        const t4a::UnitPlan& up, unsigned int output_len) {
   constexpr bool kFloat = std::is_same_v<T, float> || std::is_same_v<T, double>;
   constexpr bool kOrdered = kFloat || std::is_same_v<T, int> || std::is_same_v<T, long long>;
+  // Several planes a block (block.y > 1): 32-lane planes of at most 8-byte
+  // elements over a strided axis one thread per output (neighbouring outputs'
+  // loads coalesce: 2^20 outputs over a 64-element axis 4 MiB apart, 88 us
+  // against 370 with packed planes); else the packed planes (a contiguous
+  // 64-element axis: 136 us against 375 one thread per output).
+  const bool multi = block.y > 1;
+  const bool per_thread = multi && block.x == static_cast<unsigned>(t4a::kWarp) &&
+                          sizeof(T) <= 8 && up.axis_stride != 1;
+  auto go = [&](auto fold) {
+    using Fold = decltype(fold);
+    if (per_thread)
+      hipLaunchKernelGGL((t4a::reduce_plane_thread_kernel<T, Fold>),
+                         dim3((output_len + t4a::kBlock - 1) / t4a::kBlock < grid.x * block.y
+                                  ? (output_len + t4a::kBlock - 1) / t4a::kBlock
+                                  : grid.x * block.y),
+                         dim3(t4a::kBlock), 0, s, out, in, up, output_len);
+    else if (multi)
+      hipLaunchKernelGGL((t4a::reduce_plane_multi_kernel<T, Fold>), grid, block, 0, s, out, in,
+                         up, output_len);
+    else
+      hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, Fold>), grid, block, 0, s, out, in,
+                         up, output_len);
+  };
   switch (op) {
-    case T4A_CUDA_REDUCE_SUM:
-      hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::SumFold>), grid, block, 0, s,
-                         out, in, up, output_len);
-      break;
-    case T4A_CUDA_REDUCE_PROD:
-      hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::ProdFold>), grid, block, 0, s,
-                         out, in, up, output_len);
-      break;
+    case T4A_CUDA_REDUCE_SUM: go(t4a::SumFold{}); break;
+    case T4A_CUDA_REDUCE_PROD: go(t4a::ProdFold{}); break;
     case T4A_CUDA_REDUCE_SUM_SQUARES:
-      if constexpr (kFloat)
-        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::SumSquaresFold>), grid, block,
-                           0, s, out, in, up, output_len);
+      if constexpr (kFloat) go(t4a::SumSquaresFold{});
       break;
     case T4A_CUDA_REDUCE_MAX:
-      if constexpr (kOrdered)
-        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::MaxFold>), grid, block, 0, s,
-                           out, in, up, output_len);
+      if constexpr (kOrdered) go(t4a::MaxFold{});
       break;
     case T4A_CUDA_REDUCE_MIN:
-      if constexpr (kOrdered)
-        hipLaunchKernelGGL((t4a::reduce_plane_lean_kernel<T, t4a::MinFold>), grid, block, 0, s,
-                           out, in, up, output_len);
+      if constexpr (kOrdered) go(t4a::MinFold{});
       break;
     default: break;
   }
@@ -2012,7 +2152,12 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
       launch_unit_lean<T>(op, threads, grid, block, static_cast<hipStream_t>(stream), out, in,
                           up, static_cast<unsigned int>(output_len));
     } else if (strategy == T4A_CUDA_REDUCE_PLANE && t4a::unit_plan_fits(rd, output_len) &&
-               block.y == 1 && block.z == 1 && threads <= 512u) {
+               block.z == 1 && threads <= 512u &&
+               (block.y == 1 ||
+                (block.x <= static_cast<unsigned>(t4a::kWarp) && (block.x & (block.x - 1)) == 0 &&
+                 threads == static_cast<unsigned>(t4a::kBlock) &&
+                 t4a::grid_stride_fits(output_len, grid.x,
+                                       2ull * block.y)))) {
       const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, false);
       launch_plane_lean<T>(op, grid, block, static_cast<hipStream_t>(stream), out, in, up,
                            static_cast<unsigned int>(output_len));

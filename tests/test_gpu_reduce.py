@@ -257,6 +257,32 @@ def test_unit_one_group_axes_many_outputs(dtype):
                          explicit=(t.ReduceStrategy.Unit, 32))
 
 
+@pytest.mark.parametrize("dtype,op", [(F32, Sum), (F32, Max), (F64, Prod), (I32, Sum),
+                                      (C32, Sum), (C64, Sum), (I64, Min)],
+                         ids=lambda x: x.name)
+def test_direct_plane_packed_planes(dtype, op):
+    """Direct PLANE under this build's geometry: 256 / W planes of W = 8, 16, 32
+    lanes a block (block.y), a grid of at most 4096 blocks striding over more
+    outputs than it holds planes, two outputs a plane at a time when a lane
+    holds few elements, one at a time with every load ahead, and the serial
+    walk past that, on a contiguous and on a strided axis; 32-lane planes of
+    at most 8-byte elements over a strided axis run one thread per output
+    (lane 0's fold and tree)."""
+    rng = np.random.default_rng(60 + int(dtype) + 7 * int(op))
+    ahead = 4 if dtype.size >= 16 else 8 if dtype.size >= 8 else 16
+    for w in (8, 16, 32):
+        direct_max = 16 * w - 1  # below two chunks of 8 planes: no split
+        lengths = sorted({w + 1, w * ahead // 2, w * ahead // 2 + 1,
+                          min(w * ahead + 1, direct_max), direct_max})
+        for length in lengths:
+            outputs = 40_000 if length <= 64 else 9_000
+            plan = compact_case(dtype, op, (outputs, length), 1, w, rng,
+                                explicit=(t.ReduceStrategy.Plane, w))
+            assert plan.launch.block == (w, 256 // w, 1), plan.launch
+            compact_case(dtype, op, (length, outputs), 0, w, rng,
+                         explicit=(t.ReduceStrategy.Plane, w))
+
+
 @pytest.mark.parametrize("dtype", [F32, F64, I32, I64], ids=lambda d: d.name)
 def test_unit_one_group_output_decodes(dtype):
     """The one-group kernel's two output decodes: one fused output dim with a

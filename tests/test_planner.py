@@ -191,7 +191,12 @@ def test_strategy_boundary_is_the_plane_width():
 def test_reduction_geometry_and_shapes():
     inp, out = reduced([4, 64, 2], 1)
     launch = t.plan_reduce(DType.F32, ReduceOp.Max, ReduceStrategy.Plane, out, 8, inp, 512, 1, 32)
-    assert launch.grid == (8, 1, 1) and launch.block == (32, 1, 1)  # one plane per output
+    # this build's plane geometry: 256 / W planes of W lanes a block (block.y)
+    assert launch.grid == (1, 1, 1) and launch.block == (32, 8, 1)
+    inp, out = reduced([64, 100_000], 0)
+    launch = t.plan_reduce(DType.F32, ReduceOp.Sum, ReduceStrategy.Plane, out, 100_000, inp,
+                           6_400_000, 0, 16)
+    assert launch.grid == (4096, 1, 1) and launch.block == (16, 16, 1)
     inp, out = reduced([4, 4, 2], 1)
     launch = t.plan_reduce(DType.F32, ReduceOp.Sum, ReduceStrategy.Unit, out, 8, inp, 32, 1, 8)
     # this build's unit geometry: one-wavefront blocks below 1024 * 256 outputs
@@ -232,7 +237,7 @@ def test_reduction_plan_applies_the_auto_policy():
     inp, out = reduced([64, 4], 0)
     plan = t.plan_reduction(DType.F64, ReduceOp.Sum, out, 4, inp, 256, 0, 32)
     assert plan.kind == "Direct" and plan.strategy == ReduceStrategy.Plane
-    assert plan.launch.grid == (4, 1, 1)
+    assert plan.launch.grid == (1, 1, 1) and plan.launch.block == (32, 8, 1)
     inp, out = reduced([512, 4], 0)
     plan = t.plan_reduction(DType.F64, ReduceOp.Sum, out, 4, inp, 2048, 0, 32)
     assert plan.kind == "Split" and plan.split == Split(2, 256)
@@ -241,7 +246,8 @@ def test_reduction_plan_applies_the_auto_policy():
     inp, out = reduced([8448, 2], 0)
     plan = t.plan_reduction(DType.F32, ReduceOp.SumSquares, out, 2, inp, 16896, 0, 32)
     assert plan.split.splits == 33 and plan.combine_strategy == ReduceStrategy.Plane
-    assert plan.combine_op == ReduceOp.Sum and plan.pass2.grid == (2, 1, 1)
+    assert plan.combine_op == ReduceOp.Sum and plan.pass2.grid == (1, 1, 1)
+    assert plan.pass2.block == (32, 8, 1)
 
 
 def test_partials_plans_enforce_the_floor_split():
@@ -264,9 +270,10 @@ def test_combine_pass_widens_only_for_long_partials_and_not_for_prod():
             plan = t.plan_reduction(DType.F64, op, out, 1, inp, length, 0, 32)
             assert plan.split.splits == want_splits
             assert plan.combine_strategy == ReduceStrategy.Plane
-            assert plan.pass2.block == (want_block, 1, 1)
+            # a 32-lane combine plane is packed with seven idle ones (block.y)
+            assert plan.pass2.block == ((32, 8, 1) if want_block == 32 else (want_block, 1, 1))
         plan = t.plan_reduction(DType.F64, ReduceOp.Prod, out, 1, inp, length, 0, 32)
-        assert plan.pass2.block == (32, 1, 1)
+        assert plan.pass2.block == (32, 8, 1)
 
 
 def test_wide_combine_widths_are_plane_only_and_bounded():
