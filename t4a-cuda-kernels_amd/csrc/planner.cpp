@@ -413,7 +413,7 @@ int plan_reduce(int dtype, int op, int strategy, const View& out, long long out_
     if (blocks > kPlaneMultiBlocks) blocks = kPlaneMultiBlocks;
     if (t4a::unit_plan_fits(rd, output_len) &&
         t4a::grid_stride_fits(output_len, static_cast<unsigned int>(blocks),
-                              2ull * static_cast<unsigned long long>(planes))) {
+                              4ull * static_cast<unsigned long long>(planes))) {
       launch->grid[0] = static_cast<unsigned int>(blocks);
       launch->grid[1] = launch->grid[2] = 1;
       launch->block[0] = plane_width;

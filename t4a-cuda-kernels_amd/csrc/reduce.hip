@@ -515,12 +515,12 @@ __device__ __forceinline__ void plane_body(void* out_ptr, const void* in_ptr, co
 // reductions of 33..511-element axes, where the reference geometry (one W-lane
 // block per output, which the module entry keeps) leaves half of every
 // wavefront idle and pays one block dispatch per output (2^20 outputs of a
-// 64-element f32 axis: 687 us). Plane p of block b takes outputs
-// b * planes + p + j * S (S = gridDim.x * planes), two at a time with every
-// load of both issued before the first fold when a lane holds at most
-// kAhead / 2 elements of an output; each output is folded exactly as
-// plane_body folds it: lane l seeds element l, folds l + W, l + 2W, ..., then
-// the xor tree.
+// 64-element f32 axis: 687 us). When a lane holds at most kAhead / 4 elements
+// of an output, plane q (= b * planes + p) takes runs of four consecutive
+// outputs 4q + 4jS (S = gridDim.x * planes), every load of the four issued
+// before the first fold; otherwise outputs q + jS one at a time. Each output is
+// folded exactly as plane_body folds it: lane l seeds element l, folds l + W,
+// l + 2W, ..., then the xor tree.
 template <typename Fold, typename T>
 __device__ __forceinline__ void plane_multi(T* __restrict__ out, const T* __restrict__ in,
                                             const UnitPlan& up, unsigned int output_len,
@@ -531,33 +531,35 @@ __device__ __forceinline__ void plane_multi(T* __restrict__ out, const T* __rest
   const int len = up.axis_len;
   const long long stride = up.axis_stride;
   constexpr int kAhead = sizeof(T) >= 16 ? 4 : sizeof(T) >= 8 ? 8 : 16;
-  constexpr int kHalf = kAhead / 2;
+  constexpr int kQuarter = kAhead / 4;
   unsigned int o0 = blockIdx.x * blockDim.y + threadIdx.y;
-  if (len <= w * kHalf) {
-    for (; o0 < output_len; o0 += 2 * span) {
-      T v[2][kHalf];
-      long long ob[2];
+  if (len <= w * kQuarter) {
+    // Four consecutive outputs a plane at a time (neighbours in memory on a
+    // contiguous axis), runs of four outputs S * 4 apart.
+    for (unsigned int r = o0 * 4; r < output_len; r += 4 * span) {
+      T v[4][kQuarter];
+      long long ob[4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const unsigned int o = o0 + u * span;
+      for (int u = 0; u < 4; ++u) {
+        const unsigned int o = r + u;
         long long ib;
-        unit_decode(up, o < output_len ? o : o0, &ib, &ob[u]);
+        unit_decode(up, o < output_len ? o : r, &ib, &ob[u]);
         const T* x = in + ib;
 #pragma unroll
-        for (int k = 0; k < kHalf; ++k) {
+        for (int k = 0; k < kQuarter; ++k) {
           const int i = lane + k * w;
           if (i < len) v[u][k] = x[i * stride];
         }
       }
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 4; ++u) {
         T acc = f.seed(v[u][0]);
 #pragma unroll
-        for (int k = 1; k < kHalf; ++k) {
+        for (int k = 1; k < kQuarter; ++k) {
           if (lane + k * w < len) acc = f.fold(acc, v[u][k]);
         }
         const T reduced = plane_tree(acc, w, f);
-        if (lane == 0 && o0 + u * span < output_len) out[ob[u]] = reduced;
+        if (lane == 0 && r + u < output_len) out[ob[u]] = reduced;
       }
     }
     return;
@@ -2089,7 +2091,7 @@ void launch_plane_lean(int op, dim3 grid, dim3 block, hipStream_t s, void* out, 
   // elements over a strided axis one thread per output (neighbouring outputs'
   // loads coalesce: 2^20 outputs over a 64-element axis 4 MiB apart, 88 us
   // against 370 with packed planes); else the packed planes (a contiguous
-  // 64-element axis: 136 us against 375 one thread per output).
+  // 64-element axis: 114 us against 375 one thread per output).
   const bool multi = block.y > 1;
   const bool per_thread = multi && block.x == static_cast<unsigned>(t4a::kWarp) &&
                           sizeof(T) <= 8 && up.axis_stride != 1;
@@ -2157,7 +2159,7 @@ extern "C" int t4a_hip_reduce(void* out, const void* in, int dtype, int op, int 
                 (block.x <= static_cast<unsigned>(t4a::kWarp) && (block.x & (block.x - 1)) == 0 &&
                  threads == static_cast<unsigned>(t4a::kBlock) &&
                  t4a::grid_stride_fits(output_len, grid.x,
-                                       2ull * block.y)))) {
+                                       4ull * block.y)))) {
       const t4a::UnitPlan up = t4a::unit_plan(rd, t4a::VecLanes<T>::value, false);
       launch_plane_lean<T>(op, grid, block, static_cast<hipStream_t>(stream), out, in, up,
                            static_cast<unsigned int>(output_len));

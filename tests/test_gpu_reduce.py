@@ -263,7 +263,7 @@ def test_unit_one_group_axes_many_outputs(dtype):
 def test_direct_plane_packed_planes(dtype, op):
     """Direct PLANE under this build's geometry: 256 / W planes of W = 8, 16, 32
     lanes a block (block.y), a grid of at most 4096 blocks striding over more
-    outputs than it holds planes, two outputs a plane at a time when a lane
+    outputs than it holds planes, runs of four outputs a plane when a lane
     holds few elements, one at a time with every load ahead, and the serial
     walk past that, on a contiguous and on a strided axis; 32-lane planes of
     at most 8-byte elements over a strided axis run one thread per output
@@ -272,8 +272,8 @@ def test_direct_plane_packed_planes(dtype, op):
     ahead = 4 if dtype.size >= 16 else 8 if dtype.size >= 8 else 16
     for w in (8, 16, 32):
         direct_max = 16 * w - 1  # below two chunks of 8 planes: no split
-        lengths = sorted({w + 1, w * ahead // 2, w * ahead // 2 + 1,
-                          min(w * ahead + 1, direct_max), direct_max})
+        cand = {w + 1, w * ahead // 4, w * ahead // 4 + 1, w * ahead + 1, direct_max}
+        lengths = sorted(n for n in cand if w <= n <= direct_max)
         for length in lengths:
             outputs = 40_000 if length <= 64 else 9_000
             plan = compact_case(dtype, op, (outputs, length), 1, w, rng,
