@@ -283,6 +283,17 @@ def test_direct_plane_packed_planes(dtype, op):
                          explicit=(t.ReduceStrategy.Plane, w))
 
 
+@pytest.mark.parametrize("dtype,op", [(F32, Sum), (F64, SumSq), (I64, Sum), (C64, Sum),
+                                      (F32, Max), (I32, Prod)], ids=lambda x: x.name)
+def test_single_output_long_chunks(dtype, op):
+    """One output over 2^22 + 13 elements (4096 chunks of about 1024, one plane
+    each, whole 4-group batches with the next batch's loads in flight, then the
+    partial batch and the tail), and over 2^20 + 5 (4096 chunks of 256)."""
+    rng = np.random.default_rng(30 + int(dtype) + 5 * int(op))
+    for n in ((1 << 22) + 13, (1 << 20) + 5):
+        compact_case(dtype, op, (n,), 0, 32, rng)
+
+
 @pytest.mark.parametrize("dtype", [F32, F64, I32, I64], ids=lambda d: d.name)
 def test_unit_one_group_output_decodes(dtype):
     """The one-group kernel's two output decodes: one fused output dim with a
