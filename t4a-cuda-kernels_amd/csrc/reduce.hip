@@ -374,9 +374,12 @@ __device__ __forceinline__ void unit_lean(T* __restrict__ out, const T* __restri
         const Group<T, V>* g = reinterpret_cast<const Group<T, V>*>(x);
         const int groups = len / V;
         T acc;
-        constexpr int kShort = 16;
-        if (BS != kBlock && groups <= kShort) {
-          // a short axis (combine passes): every load before the first fold
+        // A short axis: every load before the first fold (combine passes: up
+        // to 16 groups; the large grids up to 8, e.g. 2^22 outputs over a
+        // 16-element f32 axis, whose lanes otherwise wait on each group in
+        // turn).
+        constexpr int kShort = BS != kBlock ? 16 : 8;
+        if (groups <= kShort) {
           Group<T, V> v[kShort];
 #pragma unroll
           for (int k = 0; k < kShort; ++k) {

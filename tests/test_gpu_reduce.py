@@ -283,6 +283,21 @@ def test_direct_plane_packed_planes(dtype, op):
                          explicit=(t.ReduceStrategy.Plane, w))
 
 
+@pytest.mark.parametrize("dtype", [F32, F64, I32, I64], ids=lambda d: d.name)
+def test_unit_short_contiguous_axes_many_outputs(dtype):
+    """Unit reductions over contiguous axes of 2 to 9 16-byte groups with
+    enough outputs for 256-thread blocks: up to 8 groups every load before the
+    first fold, past that group by group, tails after the last whole group."""
+    rng = np.random.default_rng(70 + int(dtype))
+    v = 16 // dtype.size
+    for length in sorted({2 * v, 3 * v + 1, min(8 * v, 32), 8 * v + 3, 9 * v}):
+        if length > 32:
+            continue
+        for op in (Sum, Max):
+            compact_case(dtype, op, (300_007, length), 1, 32, rng,
+                         explicit=(t.ReduceStrategy.Unit, 32))
+
+
 @pytest.mark.parametrize("dtype,op", [(F32, Sum), (F64, SumSq), (I64, Sum), (C64, Sum),
                                       (F32, Max), (I32, Prod)], ids=lambda x: x.name)
 def test_single_output_long_chunks(dtype, op):
